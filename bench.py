@@ -1,0 +1,250 @@
+"""Benchmark of the SushiBLAS GEMM hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): fp32 GEMM, row-major, no
+transpose, M = N = K = 8192, alpha = 1.5, beta = 0.5; A, B ~ U[-1, 1) and
+C ~ N(0, 1) from the Philox4x32-10 generator (seed 20261203), generated in
+HBM before timing.  A "step" is one sbx_sgemm call (include/sbx.h) over that
+problem; `value` = 2*M*N*K / (average step time), in TFLOP/s.
+
+Printed as one JSON line.  Besides the contract fields it carries:
+  roofline      -- the dominant kernel against the fp32 MFMA peak
+  cpu_baseline  -- the CPU oracle (oracle/, a port: the reference's oneMKL
+                   SYCL path cannot be built here) timed on a bounded sample of
+                   rows of the same problem, on this host's cores
+  parity        -- normwise error of the GPU result vs the oracle on the
+                   sampled rows (identical input bits)
+  also          -- the other BASELINE configs timed the same way (fp64 8192^3,
+                   the ragged 4095x3001x2047 transposes, tall-skinny, 512^3)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
+                       [--cpu-seconds S]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOP/s on 1 MI355X (fp32 8192³, fp64 8192³); % of MFMA peak"
+PEAK = {"f32": 157.3, "f64": 78.6}  # dense MFMA TFLOP/s, MI355X
+HBM_PEAK_GBS = 8000.0
+SEED = 20261201
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    return ap.parse_args()
+
+
+def time_launches(fn, steps, warmup):
+    """Average device time per call of fn() over `steps` back-to-back calls,
+    measured with HIP events on the stream the kernels run on."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms
+
+
+def read_traffic(kernel_name):
+    """HBM bytes per launch of `kernel_name` from the committed rocprofv3 PMC
+    summary (profiles/hbm_traffic.md), or None if it was not measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 2 and cells[0] == kernel_name:
+            try:
+                return int(cells[-1])
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(A, B, C0, m, n, k, alpha, beta, got_full, target_s):
+    """Oracle (port, fp32 accumulation) on the first R rows of the problem."""
+    import numpy as np
+    import oracle
+    threads = oracle.num_threads()
+    # calibrate on 64 rows, then size the sample to ~target_s seconds
+    r0 = 64
+    Cs = np.array(C0[:r0 * n], copy=True)
+    t = time.perf_counter()
+    oracle.gemm(0, 0, 0, r0, n, k, alpha, np.array(A[:r0 * k], copy=True), k, B, n, beta, Cs,
+                n, 0)
+    rate = 2.0 * r0 * n * k / max(time.perf_counter() - t, 1e-6)
+    rows = int(min(m, max(r0, (rate * target_s) / (2.0 * n * k) // 64 * 64)))
+    As = np.array(A[:rows * k], copy=True)
+    Cs = np.array(C0[:rows * n], copy=True)  # the oracle writes C in place
+    t = time.perf_counter()
+    oracle.gemm(0, 0, 0, rows, n, k, alpha, As, k, B, n, beta, Cs, n, 0)
+    dt = time.perf_counter() - t
+    value = 2.0 * rows * n * k / dt / 1e12
+    # parity on the same rows: GPU result vs oracle accumulating in double
+    Cd = np.array(C0[:rows * n], copy=True)
+    oracle.gemm(0, 0, 0, rows, n, k, alpha, As, k, B, n, beta, Cd, n, 1)
+    g = np.ascontiguousarray(got_full[:rows * n]).reshape(rows, n)
+    err_truth = oracle.rel_fro_err(g, Cd.reshape(rows, n))
+    err_port = oracle.rel_fro_err(g, Cs.reshape(rows, n))
+    base = {"value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"first {rows} of {m} rows of the same {m}x{n}x{k} fp32 GEMM "
+                      f"(oracle/sbo.c blocked OpenMP sgemm, fp32 accumulation, {dt:.1f} s)"}
+    parity = {"rows": rows, "normwise_vs_oracle_f64acc": err_truth,
+              "normwise_vs_oracle_f32acc": err_port, "tolerance": 1e-5}
+    return base, parity
+
+
+def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup, dist="uniform"):
+    """Allocate, fill and time one GEMM configuration; returns a dict."""
+    import torch
+    import sushiblas_amd as sbx
+    tdt = torch.float32 if dtype == "f32" else torch.float64
+    sdt = sbx.F32 if dtype == "f32" else sbx.F64
+    sa = (k, m) if ta else (m, k)
+    sb = (n, k) if tb else (k, n)
+    lda = sa[1] if layout == 0 else sa[0]
+    ldb = sb[1] if layout == 0 else sb[0]
+    ldc = n if layout == 0 else m
+    A = torch.empty(m * k, dtype=tdt, device="cuda")
+    B = torch.empty(k * n, dtype=tdt, device="cuda")
+    C = torch.empty(m * n, dtype=tdt, device="cuda")
+    if dist == "tall_skinny":
+        sbx.fill_normal(A, seed, 0)
+        sbx.fill_normal(B, seed, 1, 1.0 / k ** 0.5)
+        C.zero_()
+    else:
+        sbx.fill_uniform(A, seed, 0)
+        sbx.fill_uniform(B, seed, 1)
+        if dist == "normal_c":
+            sbx.fill_normal(C, seed, 2)
+        else:
+            sbx.fill_uniform(C, seed, 2)
+    name = sbx.gemm_select(sdt, layout, ta, tb, m, n, k, lda, ldb, ldc)
+
+    def step():
+        sbx.gemm_ex(sdt, layout, ta, tb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0)
+
+    ms = time_launches(step, steps, warmup)
+    flops = 2.0 * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    nbytes = (m * k + k * n + m * n * (2 if beta != 0 else 1)) * A.element_size()
+    out = {"kernel": name, "ms": round(ms, 4), "tflops": round(tflops, 3),
+           "pct_peak": round(100 * tflops / PEAK[dtype], 2),
+           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    del A, B, C
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import sushiblas_amd as sbx
+    sbx.lib()
+
+    m = n = k = 8192
+    alpha, beta = 1.5, 0.5
+    seed = SEED + 2
+    A = torch.empty(m * k, dtype=torch.float32, device="cuda")
+    B = torch.empty(k * n, dtype=torch.float32, device="cuda")
+    C = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    sbx.fill_uniform(A, seed, 0)
+    sbx.fill_uniform(B, seed, 1)
+    sbx.fill_normal(C, seed, 2)
+    torch.cuda.synchronize()
+    kernel = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+
+    # one call on the initial C for the parity check / CPU baseline
+    need_host = not args.no_cpu
+    if need_host:
+        A_h = A.cpu().numpy()
+        B_h = B.cpu().numpy()
+        C0_h = C.cpu().numpy()
+    sbx.sgemm(0, 0, 0, m, n, k, alpha, A, k, B, n, beta, C, n)
+    torch.cuda.synchronize()
+    if need_host:
+        got_h = C.cpu().numpy()
+
+    def step():
+        sbx.sgemm(0, 0, 0, m, n, k, alpha, A, k, B, n, beta, C, n)
+
+    ms = time_launches(step, args.steps, args.warmup)
+    flops = 2.0 * m * n * k
+    value = flops / (ms * 1e-3) / 1e12
+    traffic = read_traffic(kernel)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: Philox4x32-10 A,B ~ U[-1,1), C ~ N(0,1), seed 20261203, in HBM",
+        "config": {"workload": "fp32 GEMM C = 1.5*A*B + 0.5*C, row-major, no transpose, "
+                               "M=N=K=8192 (BASELINE configs[1])",
+                   "m": m, "n": n, "k": k, "alpha": alpha, "beta": beta, "kernel": kernel},
+        "roofline": {"bound": "mfma", "achieved": round(value, 3), "peak": PEAK["f32"],
+                     "unit": "TFLOP/s", "frac": round(value / PEAK["f32"], 4),
+                     "traffic": traffic},
+    }
+    if need_host:
+        del A, B
+        torch.cuda.empty_cache()
+        base, parity = cpu_baseline(A_h, B_h, C0_h, m, n, k, alpha, beta, got_h,
+                                    args.cpu_seconds)
+        result["cpu_baseline"] = base
+        result["parity"] = parity
+    else:
+        result["cpu_baseline"] = None
+    del C
+    torch.cuda.empty_cache()
+
+    if not args.no_also:
+        steps = max(3, min(args.steps, 10))
+        also = {}
+        also["fp64_8192_cfg5"] = run_config("f64", 0, 0, 0, 8192, 8192, 8192, 1.0, 0.0,
+                                            SEED + 5, steps, 2)
+        for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+            also[f"fp32_ragged_cfg3_t{ta}{tb}"] = run_config(
+                "f32", 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3, steps, 2)
+        ts = run_config("f32", 0, 0, 0, 65536, 64, 4096, 1.0, 0.0, SEED + 4, steps, 2,
+                        dist="tall_skinny")
+        ts["hbm_frac"] = round(ts["hbm_gbs"] / HBM_PEAK_GBS, 4)
+        also["fp32_tall_skinny_cfg4"] = ts
+        also["fp32_512_cfg1"] = run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
+                                           steps * 5, 5)
+        result["also"] = also
+    print(json.dumps(result), flush=True)
+    del np
+
+
+if __name__ == "__main__":
+    main()

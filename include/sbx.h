@@ -1,0 +1,118 @@
+/*
+ * sbx.h -- C ABI of the MI355X (gfx950) GEMM hot path of SushiBLAS.
+ *
+ * This is the drop-in boundary.  In the reference, Level3::gemm
+ * (src/ops/blas/level3/gemm.cpp:82-198) records a task whose body,
+ * gemm_dispatch<T> (gemm.cpp:44-79), calls oneMKL on a sycl::queue.  Each
+ * entry point below replaces one of those oneMKL calls one-for-one: the same
+ * argument set as gemm_dispatch (gemm.cpp:45-51), with the sycl::queue
+ * replaced by a hipStream_t and the dependency-event vector replaced by
+ * stream order.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only; every buffer is caller-owned device
+ *     memory (or pinned host memory mapped into the device address space).
+ *     The library never frees or retains a caller pointer.
+ *   - Launches are asynchronous on `stream` (NULL = the null stream of the
+ *     current device).  Nothing is allocated on the GEMM path.
+ *   - Return value is a status code (sbx_status); nothing throws across the
+ *     ABI.  The C++ layer turns codes into std::runtime_error, as the
+ *     reference's SB_THROW_IF does (include/SushiBLAS/core/logger.hpp:316-323).
+ *   - BLAS semantics: m == 0 || n == 0 is a no-op; alpha == 0 || k == 0 gives
+ *     C = beta*C; beta == 0 means C is never read (NaN/Inf in C do not
+ *     propagate).
+ *   - layout 0 = row-major, 1 = column-major (Core::Layout,
+ *     include/SushiBLAS/core/common.hpp:41-45).  transA/transB: 0 or 1.
+ *   - Re-entrant: no mutable global state; safe to call from any host thread
+ *     (the reference runs the GEMM closure on a scheduler worker thread).
+ */
+#ifndef SBX_H
+#define SBX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum sbx_status {
+    SBX_OK = 0,
+    SBX_INVALID_ARGUMENT = 1, /* bad layout/trans flag, negative size, ld too small, null ptr */
+    SBX_UNSUPPORTED = 2,      /* dtype or shape this build cannot run                       */
+    SBX_HIP_ERROR = 3         /* a HIP runtime call or kernel launch failed                */
+} sbx_status;
+
+typedef enum sbx_dtype { SBX_F32 = 0, SBX_F64 = 1 } sbx_dtype;
+
+/* Replaces oneapi::mkl::blas::row_major::gemm<float> (gemm.cpp:63) and
+ * column_major::gemm<float> (gemm.cpp:76), reached from the FLOAT32 case of
+ * Level3::gemm (gemm.cpp:146-157). */
+int sbx_sgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              float alpha, const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+              float* C, int64_t ldc);
+
+/* Replaces row_major::gemm<double> (gemm.cpp:63) / column_major::gemm<double>
+ * (gemm.cpp:76), reached from the FLOAT64 case (gemm.cpp:158-169), where the
+ * float alpha/beta are widened to double (gemm.cpp:161). */
+int sbx_dgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              double alpha, const double* A, int64_t lda, const double* B, int64_t ldb,
+              double beta, double* C, int64_t ldc);
+
+/* Replaces row_major::gemm_batch<float> (gemm.cpp:58) and
+ * column_major::gemm_batch<float> (gemm.cpp:71): `batch` problems, problem b
+ * using A + b*str_a, B + b*str_b, C + b*str_c (strides in elements, as
+ * derived at gemm.cpp:103-105). */
+int sbx_sgemm_strided_batched(void* stream, int layout, int transA, int transB, int64_t m,
+                              int64_t n, int64_t k, float alpha, const float* A, int64_t lda,
+                              int64_t str_a, const float* B, int64_t ldb, int64_t str_b,
+                              float beta, float* C, int64_t ldc, int64_t str_c, int64_t batch);
+
+/* Replaces row_major::gemm_batch<double> (gemm.cpp:58) / column_major::gemm_batch<double>
+ * (gemm.cpp:71). */
+int sbx_dgemm_strided_batched(void* stream, int layout, int transA, int transB, int64_t m,
+                              int64_t n, int64_t k, double alpha, const double* A, int64_t lda,
+                              int64_t str_a, const double* B, int64_t ldb, int64_t str_b,
+                              double beta, double* C, int64_t ldc, int64_t str_c,
+                              int64_t batch);
+
+/* Algorithm override for tests and tuning (no counterpart in the reference,
+ * where oneMKL chooses internally): SBX_ALGO_AUTO is what the four entry
+ * points above use. */
+typedef enum sbx_algo { SBX_ALGO_AUTO = 0, SBX_ALGO_GENERIC = 1, SBX_ALGO_MFMA = 2 } sbx_algo;
+
+/* dtype-generic form of the four entry points above; alpha/beta point to a
+ * float (SBX_F32) or double (SBX_F64). */
+int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo);
+
+/* Name of the kernel the dispatcher would launch for this problem (tiling
+ * heuristics introspection for benchmarks).  Pointers are assumed 16-byte
+ * aligned.  Writes a NUL-terminated string of at most cap bytes. */
+int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                    int64_t k, int64_t lda, int64_t ldb, int64_t ldc, char* name, size_t cap);
+
+/* Human-readable text for a status code (static storage). */
+const char* sbx_status_string(int status);
+
+/* Synthetic-input generators (Philox4x32-10, counter-based), writing n
+ * elements of dtype into device memory on `stream`.  They stand in for the
+ * reference's RandomOps::uniform / normal (src/ops/math/random/uniform.cpp:40-62)
+ * only as a source of benchmark inputs; the stream layout is this library's
+ * own: key = seed, counter = (element block, stream_id, 0).
+ * uniform: [-1, 1).  normal: N(0, 1) * scale. */
+int sbx_fill_uniform(void* stream, int dtype, void* out, int64_t n, uint64_t seed,
+                     uint32_t stream_id);
+int sbx_fill_normal(void* stream, int dtype, void* out, int64_t n, uint64_t seed,
+                    uint32_t stream_id, double scale);
+
+/* Library version string. */
+const char* sbx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SBX_H */

@@ -1,0 +1,158 @@
+"""sushiblas_amd -- MI355X (gfx950) GEMM hot path of SushiBLAS.
+
+The product is the HIP library ``lib/libsbx.so`` behind the C ABI declared in
+``include/sbx.h``, plus the C++ Engine/Tensor/Storage layer in ``cpp/`` that
+mirrors the reference's API (``Level3::gemm``, src/ops/blas/level3/gemm.cpp:82).
+This module is a thin ctypes binding of the C ABI for Python callers (tests,
+benchmarks): device buffers are passed as raw pointers (ints) or torch tensors
+(their ``data_ptr()``), and the stream defaults to torch's current stream.
+
+There is no CPU fallback: if the HIP library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libsbx.so")
+
+F32, F64 = 0, 1
+ALGO_AUTO, ALGO_GENERIC, ALGO_MFMA = 0, 1, 2
+STATUS = {0: "SBX_OK", 1: "SBX_INVALID_ARGUMENT", 2: "SBX_UNSUPPORTED", 3: "SBX_HIP_ERROR"}
+
+_lib = None
+
+
+class SbxError(RuntimeError):
+    """Raised when an sbx_* entry point returns a non-zero status."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where} failed: {STATUS.get(status, status)} ({_status_text(status)})")
+
+
+def build(force: bool = True, jobs: int = 8) -> None:
+    """Compile the HIP library in-tree (hipcc --offload-arch=gfx950)."""
+    args = ["make", "-C", _HERE, f"-j{jobs}"] + (["-B"] if force else [])
+    res = subprocess.run(args, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("building libsbx.so failed:\n" + res.stdout[-4000:])
+
+
+def lib() -> ctypes.CDLL:
+    """Load libsbx.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                           "(or `make -C sushiblas_amd`) first")
+    L = ctypes.CDLL(LIB_PATH)
+    i64, vp, i32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+    L.sbx_gemm_ex.restype = i32
+    L.sbx_gemm_ex.argtypes = [vp, i32, i32, i32, i32, i64, i64, i64, vp, vp, i64, i64, vp, i64,
+                              i64, vp, vp, i64, i64, i64, i32]
+    for name, real in (("sbx_sgemm", ctypes.c_float), ("sbx_dgemm", ctypes.c_double)):
+        f = getattr(L, name)
+        f.restype = i32
+        f.argtypes = [vp, i32, i32, i32, i64, i64, i64, real, vp, i64, vp, i64, real, vp, i64]
+    for name, real in (("sbx_sgemm_strided_batched", ctypes.c_float),
+                       ("sbx_dgemm_strided_batched", ctypes.c_double)):
+        f = getattr(L, name)
+        f.restype = i32
+        f.argtypes = [vp, i32, i32, i32, i64, i64, i64, real, vp, i64, i64, vp, i64, i64, real,
+                      vp, i64, i64, i64]
+    L.sbx_gemm_select.restype = i32
+    L.sbx_gemm_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64,
+                                  ctypes.c_char_p, ctypes.c_size_t]
+    L.sbx_status_string.restype = ctypes.c_char_p
+    L.sbx_status_string.argtypes = [i32]
+    L.sbx_fill_uniform.restype = i32
+    L.sbx_fill_uniform.argtypes = [vp, i32, vp, i64, ctypes.c_uint64, ctypes.c_uint32]
+    L.sbx_fill_normal.restype = i32
+    L.sbx_fill_normal.argtypes = [vp, i32, vp, i64, ctypes.c_uint64, ctypes.c_uint32,
+                                  ctypes.c_double]
+    L.sbx_version.restype = ctypes.c_char_p
+    L.sbx_version.argtypes = []
+    _lib = L
+    return L
+
+
+def _status_text(status: int) -> str:
+    try:
+        return lib().sbx_status_string(status).decode()
+    except Exception:  # pragma: no cover - only when the library itself is absent
+        return "?"
+
+
+def _ptr(x) -> int:
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    return int(x.data_ptr())
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        import torch
+        return int(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+def _check(status: int, where: str) -> None:
+    if status != 0:
+        raise SbxError(status, where)
+
+
+def gemm_ex(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb, str_b, beta,
+            C, ldc, str_c, batch=1, algo=ALGO_AUTO, stream=None) -> None:
+    """sbx_gemm_ex: dtype-generic, optionally batched, with an algorithm override."""
+    real = ctypes.c_float if dtype == F32 else ctypes.c_double
+    a = real(alpha)
+    b = real(beta)
+    st = lib().sbx_gemm_ex(_stream(stream), dtype, int(layout), int(transA), int(transB), m, n,
+                           k, ctypes.byref(a), _ptr(A), lda, str_a, _ptr(B), ldb, str_b,
+                           ctypes.byref(b), _ptr(C), ldc, str_c, batch, algo)
+    _check(st, "sbx_gemm_ex")
+
+
+def sgemm(layout, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+          stream=None) -> None:
+    _check(lib().sbx_sgemm(_stream(stream), int(layout), int(transA), int(transB), m, n, k,
+                           alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc), "sbx_sgemm")
+
+
+def dgemm(layout, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+          stream=None) -> None:
+    _check(lib().sbx_dgemm(_stream(stream), int(layout), int(transA), int(transB), m, n, k,
+                           alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc), "sbx_dgemm")
+
+
+def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc) -> str:
+    buf = ctypes.create_string_buffer(128)
+    _check(lib().sbx_gemm_select(dtype, layout, int(transA), int(transB), m, n, k, lda, ldb,
+                                 ldc, buf, 128), "sbx_gemm_select")
+    return buf.value.decode()
+
+
+def fill_uniform(t, seed: int, stream_id: int, stream=None) -> None:
+    """Fill a float32/float64 device tensor with Philox uniform [-1, 1)."""
+    dtype = F32 if t.element_size() == 4 else F64
+    _check(lib().sbx_fill_uniform(_stream(stream), dtype, _ptr(t), t.numel(), seed, stream_id),
+           "sbx_fill_uniform")
+
+
+def fill_normal(t, seed: int, stream_id: int, scale: float = 1.0, stream=None) -> None:
+    """Fill a float32/float64 device tensor with Philox N(0, 1) * scale."""
+    dtype = F32 if t.element_size() == 4 else F64
+    _check(lib().sbx_fill_normal(_stream(stream), dtype, _ptr(t), t.numel(), seed, stream_id,
+                                 scale), "sbx_fill_normal")
+
+
+def version() -> str:
+    return lib().sbx_version().decode()

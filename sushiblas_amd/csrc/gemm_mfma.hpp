@@ -1,0 +1,403 @@
+// gemm_mfma.hpp -- gfx950 (CDNA4) MFMA GEMM kernel template for fp32 and fp64.
+//
+// Computes, for row-major storage (column-major calls are mapped onto this by
+// the dispatcher with C^T = op(B)^T op(A)^T):
+//     C[m][n] = alpha * sum_k op(A)[m][k] * op(B)[k][n] + beta * C[m][n]
+// which is the arithmetic the reference hands to oneMKL's
+// row_major::gemm / gemm_batch (src/ops/blas/level3/gemm.cpp:58,63).
+//
+// Design (one workgroup = 4 wave64s = 256 lanes, one macro tile BM x BN):
+//  * Operands go global -> VGPR staging -> LDS -> VGPR fragments -> MFMA.
+//    Each operand keeps in LDS the layout it has in global memory, so every
+//    global read is a coalesced 16/8/4-byte buffer load along the contiguous
+//    dimension and every LDS write is a straight vector store (no transposing
+//    scatter):
+//      "k-contiguous"  tile (A not transposed / B transposed): [X][BK + PAD]
+//      "x-contiguous"  tile (A transposed / B not transposed): [BK][X]
+//  * Fragments are read with one 16-byte LDS read per lane.  The MFMA k index
+//    is a permutation of the real k inside each group of 8: lane group q at
+//    MFMA step kk uses k = 8g + V*q + kk (V = 16 bytes / sizeof(T)).  For an
+//    x-contiguous tile, U neighbouring MFMA blocks are interleaved (block u
+//    owns rows U*i + u) so that one 16-byte read feeds U blocks.
+//  * Masking: loads go through buffer resources whose base moves with the
+//    tile; an element outside [0,M)x[0,K) (or [0,K)x[0,N)) gets the offset
+//    0x80000000, which the buffer unit turns into a zero.  Ragged M/N/K and
+//    unaligned leading dimensions (vector width 1) need no separate kernel.
+//  * LDS is double-buffered: the global loads for tile t+1 are issued before
+//    the MFMAs of tile t, stored to the other LDS buffer after them, and one
+//    barrier per k-tile separates producer and consumer.
+//  * The 1-D grid is remapped so that consecutive tiles land on the same XCD
+//    (hardware deals workgroups round-robin over the 8 XCDs) and, inside an
+//    XCD, walk a GROUP_M-tall column of tiles so that A row-panels and B
+//    column-panels are shared through that XCD's L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sbx {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// MFMA shapes.  fp32: v_mfma_f32_32x32x2_f32, fp64: v_mfma_f64_16x16x4_f64.
+//   A operand: lane l holds A[i = l % MB][k = l / MB]
+//   B operand: lane l holds B[k = l / MB][j = l % MB]
+//   D: lane l, accumulator r holds D[row(r, l / MB)][l % MB]
+//   (all three layouts were confirmed on the device with one-hot probes)
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<float> {
+    static constexpr int MB = 32;    // output block edge
+    static constexpr int Q = 2;      // lane groups along k (= MFMA k)
+    static constexpr int V = 4;      // elements per 16-byte read
+    static constexpr int NACC = 16;  // accumulators per lane
+    typedef f32x16 acc_t;
+    __device__ static inline acc_t mma(float a, float b, acc_t c)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static inline int row(int r, int q) { return 8 * (r >> 2) + 4 * q + (r & 3); }
+};
+
+template <>
+struct Mfma<double> {
+    static constexpr int MB = 16;
+    static constexpr int Q = 4;
+    static constexpr int V = 2;
+    static constexpr int NACC = 4;
+    typedef f64x4 acc_t;
+    __device__ static inline acc_t mma(double a, double b, acc_t c)
+    {
+        return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+    }
+    // measured on gfx950 with one-hot operands: row i sits in lane group i % 4,
+    // accumulator i / 4 (unlike the fp32 16x16x4 form)
+    __device__ static inline int row(int r, int q) { return q + 4 * r; }
+};
+
+// Raw buffer loads of 4/8/16 bytes.
+template <int BYTES>
+struct Raw;
+template <>
+struct Raw<4> {
+    typedef uint32_t type;
+    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
+    {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    }
+};
+template <>
+struct Raw<8> {
+    typedef u32x2 type;
+    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
+    {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    }
+};
+template <>
+struct Raw<16> {
+    typedef u32x4 type;
+    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
+    {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    }
+};
+
+// Typed N-element LDS vector read (N * sizeof(T) in {4, 8, 16}).
+template <typename T, int N>
+struct LdsVec;
+template <>
+struct LdsVec<float, 1> {
+    __device__ static inline void read(const float* p, float* o) { o[0] = *p; }
+};
+template <>
+struct LdsVec<float, 2> {
+    __device__ static inline void read(const float* p, float* o)
+    {
+        f32x2 v = *reinterpret_cast<const f32x2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    }
+};
+template <>
+struct LdsVec<float, 4> {
+    __device__ static inline void read(const float* p, float* o)
+    {
+        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+};
+template <>
+struct LdsVec<double, 1> {
+    __device__ static inline void read(const double* p, double* o) { o[0] = *p; }
+};
+template <>
+struct LdsVec<double, 2> {
+    __device__ static inline void read(const double* p, double* o)
+    {
+        f64x2 v = *reinterpret_cast<const f64x2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    }
+};
+
+// Buffer resource word 3 for gfx9-family raw buffers (32-bit dword format).
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kOobOffset = static_cast<int>(0x80000000u);
+constexpr int64_t kMaxRecords = 0x7ffffff0;
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes)
+{
+    int64_t n = bytes < 0 ? 0 : (bytes > kMaxRecords ? kMaxRecords : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n,
+                                             kRsrcWord3);
+}
+
+template <typename T>
+struct GemmArgs {
+    const T* A;
+    const T* B;
+    T* C;
+    int64_t lda, ldb, ldc;
+    int64_t str_a, str_b, str_c;  // batch strides in elements (grid z)
+    int M, N, K;
+    T alpha, beta;
+    int tiles_m, tiles_n;
+    int group_m;
+};
+
+// ---------------------------------------------------------------------------
+// One operand's global -> LDS pipeline.
+//   KC: the operand's k index is contiguous in memory (tile [X][BK+PAD]).
+//   X : tile extent along m (for A) or n (for B).
+//   VEC: elements per global load (1, or 16 bytes / sizeof(T)).
+// ---------------------------------------------------------------------------
+template <typename T, int X, int BK, bool KC, int VEC>
+struct Operand {
+    static constexpr int V = 16 / (int)sizeof(T);
+    static constexpr int PAD = KC ? V : 0;
+    static constexpr int LD = KC ? BK + PAD : X + PAD;          // LDS row pitch (elements)
+    static constexpr int ELEMS = KC ? X * LD : BK * LD;         // LDS tile size (elements)
+    static constexpr int CONTIG = KC ? BK : X;                   // contiguous extent of tile
+    static constexpr int VPR = CONTIG / VEC;                     // vectors per tile row
+    static constexpr int NV = X * BK / (VEC * 256);              // vectors per thread
+    static_assert(X * BK % (VEC * 256) == 0, "tile not divisible over 256 lanes");
+    typedef typename Raw<VEC * sizeof(T)>::type raw_t;
+
+    int off[NV];       // byte offset of each vector relative to the tile base
+    int lds_off[NV];   // element offset in the LDS tile
+    int kidx[NV];      // k index of each vector within the tile
+    bool xok[NV];      // row/column validity along X (fixed for the block)
+    raw_t stage[NV];
+
+    __device__ inline void init(int tid, int64_t ld, int x_rem)
+    {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            int v = j * 256 + tid;
+            int r = v / VPR;
+            int c = (v % VPR) * VEC;
+            off[j] = (int)((int64_t)r * ld + c) * (int)sizeof(T);
+            lds_off[j] = r * LD + c;
+            if (KC) {  // r: x index, c: k index
+                kidx[j] = c;
+                xok[j] = r < x_rem;
+            } else {   // r: k index, c: x index
+                kidx[j] = r;
+                xok[j] = c < x_rem;
+            }
+        }
+    }
+
+    __device__ inline void load(__amdgpu_buffer_rsrc_t rs, int k_rem)
+    {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            bool ok = xok[j] && kidx[j] < k_rem;
+            stage[j] = Raw<VEC * sizeof(T)>::load(rs, ok ? off[j] : kOobOffset);
+        }
+    }
+
+    __device__ inline void store(T* lds)
+    {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) *reinterpret_cast<raw_t*>(lds + lds_off[j]) = stage[j];
+    }
+};
+
+// Fragment reader for one operand of one wave: NB blocks of MB along X.
+template <typename T, int NB, bool KC, int LD>
+struct Frag {
+    static constexpr int MB = Mfma<T>::MB;
+    static constexpr int V = Mfma<T>::V;
+    static constexpr int U = KC ? 1 : (NB < V ? NB : V);  // interleave factor
+    static_assert(NB % U == 0, "block count must be a multiple of the interleave");
+
+    // Read the fragments of k-group g (8 k values) for wave offset w0.
+    // f[b][kk] is block b's operand for MFMA step kk.
+    __device__ static inline void read(const T* lds, int w0, int g, int lane, T (&f)[NB][V])
+    {
+        const int i = lane % MB, q = lane / MB;
+        if (KC) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                LdsVec<T, V>::read(lds + (w0 + b * MB + i) * LD + g * 8 + q * V, f[b]);
+        } else {
+#pragma unroll
+            for (int s = 0; s < NB / U; ++s)
+#pragma unroll
+                for (int kk = 0; kk < V; ++kk) {
+                    T t[U];
+                    LdsVec<T, U>::read(lds + (g * 8 + q * V + kk) * LD + w0 + s * U * MB + U * i, t);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) f[s * U + u][kk] = t[u];
+                }
+        }
+    }
+
+    // X index (inside the wave tile) of row/column i of block b.
+    __device__ static inline int map(int b, int i)
+    {
+        return KC ? b * MB + i : (b / U) * U * MB + U * i + (b % U);
+    }
+};
+
+template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
+          int VA, int VB>
+__global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(GemmArgs<T> p)
+{
+    typedef Mfma<T> MF;
+    constexpr int MB = MF::MB;
+    constexpr int V = MF::V;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int NBM = WTM / MB, NBN = WTN / MB;
+    static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+    static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
+    typedef Operand<T, BM, BK, A_KC, VA> OpA;
+    typedef Operand<T, BN, BK, B_KC, VB> OpB;
+    typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
+    typedef Frag<T, NBN, B_KC, OpB::LD> FragB;
+
+    __shared__ __attribute__((aligned(16))) T smem[2 * (OpA::ELEMS + OpB::ELEMS)];
+    // buffer b of A at smem + b*ELEMS_A, of B at smem + 2*ELEMS_A + b*ELEMS_B
+    auto lds_a = [&](int b) { return smem + b * OpA::ELEMS; };
+    auto lds_b = [&](int b) { return smem + 2 * OpA::ELEMS + b * OpB::ELEMS; };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave / WAVES_N) * WTM;
+    const int wn0 = (wave % WAVES_N) * WTN;
+
+    // ---- tile index: XCD-aware remap, then GROUP_M-tall column walk ----
+    const int ntiles = p.tiles_m * p.tiles_n;
+    int id = blockIdx.x;
+    if ((ntiles & 7) == 0) {
+        const int per_xcd = ntiles >> 3;
+        id = (id & 7) * per_xcd + (id >> 3);
+    }
+    const int group_span = p.group_m * p.tiles_n;
+    const int group = id / group_span;
+    const int first_m = group * p.group_m;
+    const int gsize = min(p.tiles_m - first_m, p.group_m);
+    const int in_group = id - group * group_span;
+    const int tm = first_m + in_group % gsize;
+    const int tn = in_group / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int64_t bz = blockIdx.z;
+    const T* A = p.A + bz * p.str_a;
+    const T* B = p.B + bz * p.str_b;
+    T* C = p.C + bz * p.str_c;
+
+    // ---- operand tile bases and extents ----
+    // A k-contiguous: element (m, k) at m*lda + k; x-contiguous: at k*lda + m.
+    const int64_t a_span = A_KC ? ((int64_t)(p.M - 1) * p.lda + p.K) * (int64_t)sizeof(T)
+                                : ((int64_t)(p.K - 1) * p.lda + p.M) * (int64_t)sizeof(T);
+    const int64_t b_span = B_KC ? ((int64_t)(p.N - 1) * p.ldb + p.K) * (int64_t)sizeof(T)
+                                : ((int64_t)(p.K - 1) * p.ldb + p.N) * (int64_t)sizeof(T);
+    int64_t a_pos = A_KC ? (int64_t)m0 * p.lda : (int64_t)m0;  // element offset of tile origin
+    int64_t b_pos = B_KC ? (int64_t)n0 * p.ldb : (int64_t)n0;
+    const int64_t a_step = A_KC ? BK : (int64_t)BK * p.lda;
+    const int64_t b_step = B_KC ? BK : (int64_t)BK * p.ldb;
+
+    OpA opa;
+    OpB opb;
+    opa.init(tid, p.lda, p.M - m0);
+    opb.init(tid, p.ldb, p.N - n0);
+
+    typename MF::acc_t acc[NBM][NBN];
+#pragma unroll
+    for (int i = 0; i < NBM; ++i)
+#pragma unroll
+        for (int j = 0; j < NBN; ++j)
+#pragma unroll
+            for (int r = 0; r < MF::NACC; ++r) acc[i][j][r] = 0;
+
+    const int nk = (p.K + BK - 1) / BK;
+
+    opa.load(make_rsrc(A + a_pos, a_span - a_pos * (int64_t)sizeof(T)), p.K);
+    opb.load(make_rsrc(B + b_pos, b_span - b_pos * (int64_t)sizeof(T)), p.K);
+    opa.store(lds_a(0));
+    opb.store(lds_b(0));
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            a_pos += a_step;
+            b_pos += b_step;
+            const int k_rem = p.K - (kt + 1) * BK;
+            opa.load(make_rsrc(A + a_pos, a_span - a_pos * (int64_t)sizeof(T)), k_rem);
+            opb.load(make_rsrc(B + b_pos, b_span - b_pos * (int64_t)sizeof(T)), k_rem);
+        }
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            T fa[NBM][V], fb[NBN][V];
+            FragA::read(lds_a(cur), wm0, g, lane, fa);
+            FragB::read(lds_b(cur), wn0, g, lane, fb);
+#pragma unroll
+            for (int kk = 0; kk < V; ++kk)
+#pragma unroll
+                for (int i = 0; i < NBM; ++i)
+#pragma unroll
+                    for (int j = 0; j < NBN; ++j) acc[i][j] = MF::mma(fa[i][kk], fb[j][kk], acc[i][j]);
+        }
+        if (more) {
+            opa.store(lds_a(cur ^ 1));
+            opb.store(lds_b(cur ^ 1));
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: C = alpha*acc + beta*C (C is not read when beta == 0) ----
+    const int q = lane / MB, jl = lane % MB;
+    const bool read_c = p.beta != (T)0;
+#pragma unroll
+    for (int i = 0; i < NBM; ++i)
+#pragma unroll
+        for (int j = 0; j < NBN; ++j) {
+            const int n = n0 + wn0 + FragB::map(j, jl);
+#pragma unroll
+            for (int r = 0; r < MF::NACC; ++r) {
+                const int m = m0 + wm0 + FragA::map(i, MF::row(r, q));
+                if (m < p.M && n < p.N) {
+                    T* cp = C + (int64_t)m * p.ldc + n;
+                    T v = p.alpha * acc[i][j][r];
+                    if (read_c) v += p.beta * *cp;
+                    *cp = v;
+                }
+            }
+        }
+}
+
+}  // namespace sbx

@@ -1,0 +1,45 @@
+// launch.hpp -- host-side launchers for the GEMM kernels.
+//
+// launch_mfma<T, BM, BN, BK, WAVES_M, WAVES_N> picks one of the 16 compiled
+// variants (A k-contiguous or not, B k-contiguous or not, vector or scalar
+// global loads for each operand) and launches it on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "gemm_mfma.hpp"
+
+namespace sbx {
+
+template <typename T, int BM, int BN, int BK, int WM, int WN>
+hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, bool b_vec,
+                       int batch, hipStream_t stream);
+
+// Generic (non-MFMA) fallback: 64x64 tiles, 64-bit addressing, any ld.
+template <typename T>
+hipError_t launch_generic(const GemmArgs<T>& a, bool trans_a, bool trans_b, int batch,
+                          hipStream_t stream);
+
+// C <- beta*C (beta == 0 stores zeros without reading C).
+template <typename T>
+hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
+                        int batch, hipStream_t stream);
+
+// Tile configurations compiled into the library, one translation unit each
+// (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp).
+#define SBX_MFMA_CONFIGS(X)            \
+    X(float, 256, 256, 16, 2, 2)       \
+    X(float, 128, 128, 16, 2, 2)       \
+    X(float, 256, 64, 16, 4, 1)        \
+    X(float, 64, 256, 16, 1, 4)        \
+    X(double, 128, 128, 16, 2, 2)      \
+    X(double, 256, 64, 16, 4, 1)       \
+    X(double, 64, 256, 16, 1, 4)
+
+#define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN)                                                  \
+    extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN>(                                \
+        const GemmArgs<T>&, bool, bool, bool, bool, int, hipStream_t);
+SBX_MFMA_CONFIGS(SBX_EXTERN_LAUNCH)
+#undef SBX_EXTERN_LAUNCH
+
+}  // namespace sbx

@@ -1,0 +1,355 @@
+// sbx_api.hip -- the C ABI (include/sbx.h): argument validation, the
+// column-major -> row-major mapping, quick returns, and the tiling heuristics
+// that choose a kernel.  This is what gemm_dispatch<T>
+// (src/ops/blas/level3/gemm.cpp:44-79) does in the reference, with oneMKL's
+// internal kernel choice replaced by an explicit, inspectable one.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/sbx.h"
+#include "launch.hpp"
+
+namespace sbx {
+
+hipError_t launch_fill_uniform(int dtype, void* out, int64_t n, uint64_t seed, uint32_t stream,
+                               hipStream_t s);
+hipError_t launch_fill_normal(int dtype, void* out, int64_t n, uint64_t seed, uint32_t stream,
+                              double scale, hipStream_t s);
+
+namespace {
+
+constexpr int64_t kMaxDim = (int64_t)1 << 30;        // m, n, k limit (int32 tile math)
+constexpr int64_t kMaxGridZ = 65535;                  // batch chunk per launch
+
+struct Problem {
+    int dtype;
+    bool ta, tb;
+    int64_t m, n, k;
+    const void* A;
+    int64_t lda, str_a;
+    const void* B;
+    int64_t ldb, str_b;
+    void* C;
+    int64_t ldc, str_c;
+    int64_t batch;
+};
+
+// Tile configurations compiled into the library (gemm_cfg_*.hip).
+enum Cfg {
+    F32_256x256,   // square/large fp32: 4 waves of 128x128
+    F32_128x128,   // mid-size fp32: 4 waves of 64x64
+    F32_256x64,    // n <= 64 (tall-skinny): 4 waves stacked along m
+    F32_64x256,    // m <= 64
+    F64_128x128,   // fp64: 4 waves of 64x64
+    F64_256x64,
+    F64_64x256,
+    GENERIC,
+};
+
+struct CfgInfo {
+    const char* name;
+    int bm, bn, bk;
+};
+
+const CfgInfo kCfg[] = {
+    {"mfma_f32_256x256x16_w2x2", 256, 256, 16}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16},
+    {"mfma_f32_256x64x16_w4x1", 256, 64, 16},   {"mfma_f32_64x256x16_w1x4", 64, 256, 16},
+    {"mfma_f64_128x128x16_w2x2", 128, 128, 16}, {"mfma_f64_256x64x16_w4x1", 256, 64, 16},
+    {"mfma_f64_64x256x16_w1x4", 64, 256, 16},   {"generic_64x64x16", 64, 64, 16},
+};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+Cfg choose_cfg(int dtype, int64_t m, int64_t n)
+{
+    if (dtype == SBX_F32) {
+        if (n <= 64) return F32_256x64;
+        if (m <= 64) return F32_64x256;
+        if (cdiv(m, 256) * cdiv(n, 256) >= 256) return F32_256x256;
+        return F32_128x128;
+    }
+    if (n <= 64) return F64_256x64;
+    if (m <= 64) return F64_64x256;
+    return F64_128x128;
+}
+
+// Row-major operand facts for the MFMA kernels.
+//   A (m x k): k-contiguous iff not transposed; contiguous extent k or m.
+//   B (k x n): k-contiguous iff transposed;     contiguous extent k or n.
+struct OperandPlan {
+    bool kc;
+    bool vec;
+};
+
+OperandPlan plan_operand(bool kc, int64_t contig_extent, int64_t ld, int64_t stride,
+                         int64_t batch, const void* ptr, size_t elem)
+{
+    const int64_t V = 16 / (int64_t)elem;
+    bool vec = (contig_extent % V == 0) && (ld % V == 0) &&
+               ((uintptr_t)ptr % 16 == 0) && (batch <= 1 || stride % V == 0);
+    return OperandPlan{kc, vec};
+}
+
+// Largest byte offset an MFMA tile forms relative to its buffer base.
+bool offsets_fit(bool kc, int tile_x, int bk, int64_t ld, size_t elem)
+{
+    const int64_t rows = kc ? tile_x : bk;
+    const int64_t span = (rows * ld + (kc ? bk : tile_x)) * (int64_t)elem;
+    return span < (int64_t)0x7ffffff0 - 64;
+}
+
+bool mfma_feasible(const Problem& p, Cfg c)
+{
+    const CfgInfo& ci = kCfg[c];
+    const size_t elem = p.dtype == SBX_F32 ? 4 : 8;
+    return offsets_fit(!p.ta, ci.bm, ci.bk, p.lda, elem) &&
+           offsets_fit(p.tb, ci.bn, ci.bk, p.ldb, elem) &&
+           cdiv(p.m, ci.bm) * cdiv(p.n, ci.bn) < ((int64_t)1 << 31);
+}
+
+int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
+{
+    // stored matrix is rows x cols of op(X)^T if trans
+    const int64_t sr = trans ? cols : rows, sc = trans ? rows : cols;
+    const int64_t need = layout == 0 ? sc : sr;
+    return ld >= (need > 1 ? need : 1) ? SBX_OK : SBX_INVALID_ARGUMENT;
+}
+
+hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan pb,
+                      const Problem& p, int nb, hipStream_t s)
+{
+    switch (cfg) {
+    case F32_256x256:
+        return launch_mfma<float, 256, 256, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_128x128:
+        return launch_mfma<float, 128, 128, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_256x64:
+        return launch_mfma<float, 256, 64, 16, 4, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_64x256:
+        return launch_mfma<float, 64, 256, 16, 1, 4>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    default:
+        a.tiles_m = (int)cdiv(p.m, 64);
+        a.tiles_n = (int)cdiv(p.n, 64);
+        return launch_generic<float>(a, p.ta, p.tb, nb, s);
+    }
+}
+
+hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, OperandPlan pa, OperandPlan pb,
+                      const Problem& p, int nb, hipStream_t s)
+{
+    switch (cfg) {
+    case F64_128x128:
+        return launch_mfma<double, 128, 128, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F64_256x64:
+        return launch_mfma<double, 256, 64, 16, 4, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F64_64x256:
+        return launch_mfma<double, 64, 256, 16, 1, 4>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    default:
+        a.tiles_m = (int)cdiv(p.m, 64);
+        a.tiles_n = (int)cdiv(p.n, 64);
+        return launch_generic<double>(a, p.ta, p.tb, nb, s);
+    }
+}
+
+template <typename T>
+int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen)
+{
+    if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
+    const bool quick = alpha == (T)0 || p.k == 0;
+    Cfg cfg = choose_cfg(p.dtype, p.m, p.n);
+    if (algo == SBX_ALGO_GENERIC) cfg = GENERIC;
+    if (cfg != GENERIC && !mfma_feasible(p, cfg)) {
+        if (algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
+        cfg = GENERIC;
+    }
+    if (chosen) *chosen = cfg;
+    if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
+
+    for (int64_t b0 = 0; b0 < p.batch; b0 += kMaxGridZ) {
+        const int nb = (int)((p.batch - b0) < kMaxGridZ ? (p.batch - b0) : kMaxGridZ);
+        hipError_t e;
+        if (quick) {
+            e = launch_scale<T>((T*)p.C + b0 * p.str_c, p.ldc, p.str_c, p.m, p.n, beta, nb,
+                                stream);
+        } else {
+            GemmArgs<T> a;
+            a.A = (const T*)p.A + b0 * p.str_a;
+            a.B = (const T*)p.B + b0 * p.str_b;
+            a.C = (T*)p.C + b0 * p.str_c;
+            a.lda = p.lda; a.ldb = p.ldb; a.ldc = p.ldc;
+            a.str_a = p.str_a; a.str_b = p.str_b; a.str_c = p.str_c;
+            a.M = (int)p.m; a.N = (int)p.n; a.K = (int)p.k;
+            a.alpha = alpha; a.beta = beta;
+            const CfgInfo& ci = kCfg[cfg];
+            a.tiles_m = (int)cdiv(p.m, ci.bm);
+            a.tiles_n = (int)cdiv(p.n, ci.bn);
+            a.group_m = a.tiles_m < 8 ? a.tiles_m : 8;
+            const size_t elem = sizeof(T);
+            const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
+                                                a.A, elem);
+            const OperandPlan pb = plan_operand(p.tb, p.tb ? p.k : p.n, p.ldb, p.str_b, p.batch,
+                                                a.B, elem);
+            e = launch_cfg(cfg, a, pa, pb, p, nb, stream);
+        }
+        if (e != hipSuccess) return SBX_HIP_ERROR;
+    }
+    return SBX_OK;
+}
+
+int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+              int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+              int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+              void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, Cfg* chosen)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return SBX_INVALID_ARGUMENT;
+    if (algo < SBX_ALGO_AUTO || algo > SBX_ALGO_MFMA) return SBX_INVALID_ARGUMENT;
+    if (m < 0 || n < 0 || k < 0 || batch < 0) return SBX_INVALID_ARGUMENT;
+    if (m > kMaxDim || n > kMaxDim || k > kMaxDim) return SBX_UNSUPPORTED;
+    if (!alpha || !beta) return SBX_INVALID_ARGUMENT;
+    if (check_ld(layout, transA, m, k, lda) || check_ld(layout, transB, k, n, ldb) ||
+        check_ld(layout, false, m, n, ldc))
+        return SBX_INVALID_ARGUMENT;
+    if (batch > 1 && (str_a < 0 || str_b < 0 || str_c <= 0)) return SBX_INVALID_ARGUMENT;
+    const size_t elem = dtype == SBX_F32 ? 4 : 8;
+    const bool alpha0 = dtype == SBX_F32 ? *(const float*)alpha == 0.0f
+                                         : *(const double*)alpha == 0.0;
+    if (m > 0 && n > 0 && batch > 0) {
+        if (!C || (uintptr_t)C % elem) return SBX_INVALID_ARGUMENT;
+        if (k > 0 && !alpha0) {
+            if (!A || !B || (uintptr_t)A % elem || (uintptr_t)B % elem)
+                return SBX_INVALID_ARGUMENT;
+        }
+    }
+
+    // Column-major C (m x n) is row-major C^T (n x m) = op(B)^T op(A)^T: swap
+    // the operands and the sizes, keep each operand's own transpose flag.
+    Problem p;
+    p.dtype = dtype;
+    if (layout == 0) {
+        p.ta = transA; p.tb = transB; p.m = m; p.n = n;
+        p.A = A; p.lda = lda; p.str_a = str_a;
+        p.B = B; p.ldb = ldb; p.str_b = str_b;
+    } else {
+        p.ta = transB; p.tb = transA; p.m = n; p.n = m;
+        p.A = B; p.lda = ldb; p.str_a = str_b;
+        p.B = A; p.ldb = lda; p.str_b = str_a;
+    }
+    p.k = k; p.C = C; p.ldc = ldc; p.str_c = batch > 1 ? str_c : 0; p.batch = batch;
+    if (batch <= 1) { p.str_a = 0; p.str_b = 0; }
+
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SBX_F32)
+        return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen);
+    return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen);
+}
+
+}  // namespace
+}  // namespace sbx
+
+extern "C" {
+
+int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, nullptr);
+}
+
+int sbx_sgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              float alpha, const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+              float* C, int64_t ldc)
+{
+    return sbx_gemm_ex(stream, SBX_F32, layout, transA, transB, m, n, k, &alpha, A, lda, 0, B,
+                       ldb, 0, &beta, C, ldc, 0, 1, SBX_ALGO_AUTO);
+}
+
+int sbx_dgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              double alpha, const double* A, int64_t lda, const double* B, int64_t ldb,
+              double beta, double* C, int64_t ldc)
+{
+    return sbx_gemm_ex(stream, SBX_F64, layout, transA, transB, m, n, k, &alpha, A, lda, 0, B,
+                       ldb, 0, &beta, C, ldc, 0, 1, SBX_ALGO_AUTO);
+}
+
+int sbx_sgemm_strided_batched(void* stream, int layout, int transA, int transB, int64_t m,
+                              int64_t n, int64_t k, float alpha, const float* A, int64_t lda,
+                              int64_t str_a, const float* B, int64_t ldb, int64_t str_b,
+                              float beta, float* C, int64_t ldc, int64_t str_c, int64_t batch)
+{
+    return sbx_gemm_ex(stream, SBX_F32, layout, transA, transB, m, n, k, &alpha, A, lda, str_a,
+                       B, ldb, str_b, &beta, C, ldc, str_c, batch, SBX_ALGO_AUTO);
+}
+
+int sbx_dgemm_strided_batched(void* stream, int layout, int transA, int transB, int64_t m,
+                              int64_t n, int64_t k, double alpha, const double* A, int64_t lda,
+                              int64_t str_a, const double* B, int64_t ldb, int64_t str_b,
+                              double beta, double* C, int64_t ldc, int64_t str_c,
+                              int64_t batch)
+{
+    return sbx_gemm_ex(stream, SBX_F64, layout, transA, transB, m, n, k, &alpha, A, lda, str_a,
+                       B, ldb, str_b, &beta, C, ldc, str_c, batch, SBX_ALGO_AUTO);
+}
+
+int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                    int64_t k, int64_t lda, int64_t ldb, int64_t ldc, char* name, size_t cap)
+{
+    if (!name || cap == 0) return SBX_INVALID_ARGUMENT;
+    static const float one_f = 1.0f;
+    static const double one_d = 1.0;
+    const void* one = dtype == SBX_F64 ? (const void*)&one_d : (const void*)&one_f;
+    // 16-byte aligned stand-in addresses: selection never dereferences them.
+    const void* fake = (const void*)(uintptr_t)0x1000;
+    sbx::Cfg cfg = sbx::GENERIC;
+    int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda, 0,
+                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO, &cfg);
+    if (st != SBX_OK) return st;
+    snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
+    return SBX_OK;
+}
+
+const char* sbx_status_string(int status)
+{
+    switch (status) {
+    case SBX_OK: return "success";
+    case SBX_INVALID_ARGUMENT: return "invalid argument";
+    case SBX_UNSUPPORTED: return "unsupported data type or shape";
+    case SBX_HIP_ERROR: return "HIP runtime error";
+    default: return "unknown status";
+    }
+}
+
+int sbx_fill_uniform(void* stream, int dtype, void* out, int64_t n, uint64_t seed,
+                     uint32_t stream_id)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (n < 0 || (n > 0 && !out)) return SBX_INVALID_ARGUMENT;
+    if (n == 0) return SBX_OK;
+    return sbx::launch_fill_uniform(dtype, out, n, seed, stream_id, (hipStream_t)stream) ==
+                   hipSuccess
+               ? SBX_OK
+               : SBX_HIP_ERROR;
+}
+
+int sbx_fill_normal(void* stream, int dtype, void* out, int64_t n, uint64_t seed,
+                    uint32_t stream_id, double scale)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (n < 0 || (n > 0 && !out)) return SBX_INVALID_ARGUMENT;
+    if (n == 0) return SBX_OK;
+    return sbx::launch_fill_normal(dtype, out, n, seed, stream_id, scale, (hipStream_t)stream) ==
+                   hipSuccess
+               ? SBX_OK
+               : SBX_HIP_ERROR;
+}
+
+const char* sbx_version(void) { return "sushiblas_amd 0.1.0 (gfx950)"; }
+
+}  // extern "C"

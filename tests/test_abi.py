@@ -1,0 +1,106 @@
+"""CPU-side checks of the C ABI library: it loads, exports every function
+include/sbx.h declares, and its host-only logic (argument validation, status
+strings, kernel selection) behaves -- none of these launch a kernel."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import sushiblas_amd as sbx
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(sbx_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_gemm_entry_points():
+    names = declared_functions()
+    for n in ("sbx_sgemm", "sbx_dgemm", "sbx_sgemm_strided_batched",
+              "sbx_dgemm_strided_batched", "sbx_gemm_ex", "sbx_status_string"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = sbx.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), f"{name} declared in include/ but not exported"
+
+
+def test_exports_are_c_linkage():
+    out = os.popen(f"nm -D --defined-only {sbx.LIB_PATH}").read()
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}$", out, flags=re.M), name
+
+
+def test_status_strings():
+    L = sbx.lib()
+    assert L.sbx_status_string(0) == b"success"
+    assert L.sbx_status_string(1) == b"invalid argument"
+    assert L.sbx_status_string(2).startswith(b"unsupported")
+    assert L.sbx_status_string(3) == b"HIP runtime error"
+    assert L.sbx_status_string(99) == b"unknown status"
+    assert sbx.version().startswith("sushiblas_amd")
+
+
+def _call(**kw):
+    args = dict(stream=0, dtype=0, layout=0, ta=0, tb=0, m=4, n=4, k=4, A=16, lda=4, sa=0,
+                B=16, ldb=4, sb=0, C=16, ldc=4, sc=0, batch=1, algo=0)
+    args.update(kw)
+    a = ctypes.c_double(1.0) if args["dtype"] == 1 else ctypes.c_float(1.0)
+    return sbx.lib().sbx_gemm_ex(args["stream"], args["dtype"], args["layout"], args["ta"],
+                                 args["tb"], args["m"], args["n"], args["k"], ctypes.byref(a),
+                                 args["A"], args["lda"], args["sa"], args["B"], args["ldb"],
+                                 args["sb"], ctypes.byref(a), args["C"], args["ldc"], args["sc"],
+                                 args["batch"], args["algo"])
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(layout=2), 1), (dict(ta=2), 1), (dict(tb=-1), 1), (dict(m=-1), 1), (dict(k=-3), 1),
+    (dict(lda=3), 1), (dict(ldb=3), 1), (dict(ldc=3), 1), (dict(ta=1, m=8, lda=4), 1),
+    (dict(layout=1, m=8, ldc=4), 1), (dict(C=0), 1), (dict(A=0), 1), (dict(A=18), 1),
+    (dict(dtype=7), 2), (dict(algo=9), 1), (dict(batch=-1), 1),
+    (dict(batch=2, sc=0), 1), (dict(m=(1 << 31)), 2),
+])
+def test_argument_validation(kw, status):
+    """Invalid arguments are rejected on the host, before any HIP call."""
+    assert _call(**kw) == status
+
+
+def test_noop_cases_need_no_device():
+    """m == 0 / n == 0 / batch == 0 return before touching the device."""
+    assert _call(m=0) == 0
+    assert _call(n=0, ldc=1) == 0
+    assert _call(batch=0) == 0
+
+
+@pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
+    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x16_w2x2"),
+    (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2"),
+    (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_256x64x16_w4x1"),
+    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x256x16_w1x4"),
+    (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_256x64x16_w4x1"),
+    (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
+    (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_256x64x16_w4x1"),
+])
+def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
+    sa = (k, m) if ta else (m, k)
+    sbd = (n, k) if tb else (k, n)
+    lda = sa[1] if layout == 0 else sa[0]
+    ldb = sbd[1] if layout == 0 else sbd[0]
+    ldc = n if layout == 0 else m
+    assert sbx.gemm_select(dtype, layout, ta, tb, m, n, k, lda, ldb, ldc) == expect
+
+
+def test_huge_leading_dimension_falls_back_to_generic():
+    """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
+    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
+        "generic_64x64x16"

@@ -1,0 +1,311 @@
+"""GPU parity tests: the HIP GEMM kernels, called through the C ABI
+(include/sbx.h), against the CPU oracle on identical seeded inputs.
+
+Bar (from the task's tolerance): normwise relative Frobenius error
+||C_gpu - C_oracle||_F / ||C_oracle||_F <= 1e-5 (fp32) and <= 1e-12 (fp64),
+oracle accumulating in double.  Known answers are checked exactly.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from gemm_cases import (TOL, c_window, make_inputs, normwise, run_oracle, run_sbx)
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261201
+
+
+def _case(dev, dtype, layout, ta, tb, m, n, k, alpha, beta, seed, algo=0, pad=(0, 0, 0),
+          offsets=(0, 0, 0), dist="uniform"):
+    A, lda, B, ldb, C, ldc = make_inputs(dtype, layout, ta, tb, m, n, k, seed, pad, dist)
+    got = run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                  algo, offsets)
+    want = run_oracle(layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+    err = normwise(layout, got, want, m, n, ldc)
+    print(f"case dtype={np.dtype(dtype).name} layout={layout} tA={ta} tB={tb} "
+          f"m={m} n={n} k={k} alpha={alpha} beta={beta} algo={algo} err={err:.3e}", flush=True)
+    return err, got, want
+
+
+# -- reference known answers (tests/blas/level3/test_gemm.cpp:39-88) --------
+
+def test_known_answer_3x3_row_major(cuda):
+    """SimpleGEMM3x3: A = [1..9], B = 2*I, beta = 0 -> C = 2*A (exact)."""
+    A = np.arange(1, 10, dtype=np.float32)
+    B = (2 * np.eye(3, dtype=np.float32)).ravel()
+    C = np.zeros(9, np.float32)
+    got = run_sbx(cuda, np.float32, 0, 0, 0, 3, 3, 3, 1.0, A, 3, B, 3, 0.0, C, 3)
+    assert got.tolist() == [2, 4, 6, 8, 10, 12, 14, 16, 18]
+
+
+def test_known_answer_2x2_column_major(cuda):
+    """SimpleGEMMColumnMajor: memory [1,3,2,4] x [5,7,6,8] -> [19,43,22,50]."""
+    A = np.array([1, 3, 2, 4], np.float32)
+    B = np.array([5, 7, 6, 8], np.float32)
+    C = np.zeros(4, np.float32)
+    got = run_sbx(cuda, np.float32, 1, 0, 0, 2, 2, 2, 1.0, A, 2, B, 2, 0.0, C, 2)
+    assert got.tolist() == [19, 43, 22, 50]
+
+
+# -- BASELINE configurations ---------------------------------------------------
+
+def test_cfg1_fp32_512(cuda):
+    """fp32 512^3, row-major, alpha=1, beta=0, U[-1,1]."""
+    err, got, want = _case(cuda, np.float32, 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1)
+    assert err <= TOL[np.float32]
+    # also against the oracle accumulating in fp32, as a vendor sgemm does
+    A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, 512, 512, 512, SEED + 1)
+    native = run_oracle(0, 0, 0, 512, 512, 512, 1.0, A, lda, B, ldb, 0.0, C, ldc, acc_mode=0)
+    assert normwise(0, got, native, 512, 512, ldc) <= TOL[np.float32]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_cfg3_ragged_all_transposes(cuda, ta, tb):
+    """fp32 M=4095, N=3001, K=2047, alpha=beta=1, every transA/transB (masked edges)."""
+    err, _, _ = _case(cuda, np.float32, 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3)
+    assert err <= TOL[np.float32]
+
+
+def test_cfg4_tall_skinny(cuda):
+    """fp32 M=65536, K=4096, N=64, A ~ N(0,1), B ~ N(0,1)/sqrt(K): full oracle check."""
+    import torch
+    import sushiblas_amd as sbx
+    m, n, k = 65536, 64, 4096
+    A = oracle.fill_normal(m * k, np.float32, SEED + 4, 0)
+    B = oracle.fill_normal(k * n, np.float32, SEED + 4, 1, 1.0 / math.sqrt(k))
+    C = np.full(m * n, np.nan, np.float32)  # beta = 0: C must not be read
+    got = run_sbx(cuda, np.float32, 0, 0, 0, m, n, k, 1.0, A, k, B, n, 0.0, C, n)
+    want = run_oracle(0, 0, 0, m, n, k, 1.0, A, k, B, n, 0.0, C, n)
+    assert not np.isnan(got).any()
+    err = normwise(0, got, want, m, n, n)
+    print(f"tall-skinny err={err:.3e} kernel="
+          f"{sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)}")
+    assert err <= TOL[np.float32]
+    del torch
+
+
+def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c):
+    """Full-size GEMM on the GPU; oracle on a sample of rows plus a
+    Freivalds projection of the whole result (C_gpu x vs alpha A (B x) + beta C0 x)."""
+    import torch
+    import sushiblas_amd as sbx
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    dA = torch.empty(m * k, dtype=tdt, device=cuda)
+    dB = torch.empty(k * n, dtype=tdt, device=cuda)
+    dC = torch.empty(m * n, dtype=tdt, device=cuda)
+    sbx.fill_uniform(dA, seed, 0)
+    sbx.fill_uniform(dB, seed, 1)
+    if dist_c == "normal":
+        sbx.fill_normal(dC, seed, 2)
+    else:
+        sbx.fill_uniform(dC, seed, 2)
+    torch.cuda.synchronize()
+    A = dA.cpu().numpy()
+    B = dB.cpu().numpy()
+    C0 = dC.cpu().numpy()
+    sbx.gemm_ex(sbx.F32 if dtype == np.float32 else sbx.F64, 0, 0, 0, m, n, k, alpha, dA, k, 0,
+                dB, n, 0, beta, dC, n, 0)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy().reshape(m, n)
+    rows = np.unique(np.concatenate([np.arange(0, 16), np.arange(m - 16, m),
+                                     np.random.default_rng(seed).integers(0, m, 32)]))
+    Ar = np.ascontiguousarray(A.reshape(m, k)[rows]).ravel()
+    Cr = np.ascontiguousarray(C0.reshape(m, n)[rows]).ravel()
+    oracle.gemm(0, 0, 0, len(rows), n, k, alpha, Ar, k, B, n, beta, Cr, n, 1)
+    err_rows = oracle.rel_fro_err(np.ascontiguousarray(got[rows]), Cr.reshape(len(rows), n))
+    x = np.random.default_rng(seed + 7).standard_normal(n)
+    lhs = got.astype(np.float64) @ x
+    rhs = alpha * (A.reshape(m, k).astype(np.float64) @ (B.reshape(k, n).astype(np.float64) @ x))
+    rhs += beta * (C0.reshape(m, n).astype(np.float64) @ x)
+    err_proj = float(np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs))
+    print(f"{m}x{n}x{k} {np.dtype(dtype).name}: sampled-rows err={err_rows:.3e} "
+          f"Freivalds err={err_proj:.3e}", flush=True)
+    return err_rows, err_proj
+
+
+def test_cfg2_fp32_8192(cuda):
+    """fp32 8192^3, alpha=1.5, beta=0.5, C ~ N(0,1): sampled rows + Freivalds."""
+    e_rows, e_proj = _sampled_rows_check(cuda, np.float32, 8192, 8192, 8192, 1.5, 0.5,
+                                         SEED + 2, "normal")
+    assert e_rows <= TOL[np.float32]
+    assert e_proj <= TOL[np.float32]
+
+
+def test_cfg5_fp64_8192(cuda):
+    """fp64 8192^3, alpha=1, beta=0: sampled rows + Freivalds, tolerance 1e-12."""
+    e_rows, e_proj = _sampled_rows_check(cuda, np.float64, 8192, 8192, 8192, 1.0, 0.0,
+                                         SEED + 5, "uniform")
+    assert e_rows <= TOL[np.float64]
+    assert e_proj <= TOL[np.float64]
+
+
+# -- coverage sweeps -----------------------------------------------------------
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (100, 37, 129), (257, 300, 45), (37, 1000, 300),
+          (1000, 50, 300), (515, 301, 257)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sweep_shapes_layouts_transposes(cuda, dtype, layout, ta, tb):
+    for i, (m, n, k) in enumerate(SHAPES):
+        alpha, beta = (1.0, 0.0) if i % 2 == 0 else (-0.75, 1.25)
+        err, _, _ = _case(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, SEED + 10 + i)
+        assert err <= TOL[dtype], (m, n, k)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_generic_path_matches(cuda, dtype, ta, tb):
+    """The non-MFMA fallback kernel, forced through the algo override."""
+    for m, n, k in [(129, 77, 65), (300, 200, 100)]:
+        err, _, _ = _case(cuda, dtype, 0, ta, tb, m, n, k, 1.5, -0.5, SEED + 30, algo=1)
+        assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_padded_ld_and_unaligned_pointers(cuda, dtype):
+    """ld larger than the minimum and base pointers off 16-byte alignment
+    (forces the scalar-load variants)."""
+    for ta, tb in [(0, 0), (1, 0), (0, 1), (1, 1)]:
+        err, _, _ = _case(cuda, dtype, 0, ta, tb, 260, 196, 132, 1.0, 0.5, SEED + 40,
+                          pad=(3, 5, 7), offsets=(1, 3, 1))
+        assert err <= TOL[dtype]
+        err, _, _ = _case(cuda, dtype, 0, ta, tb, 256, 256, 128, 1.0, 0.0, SEED + 41,
+                          pad=(4, 8, 4))
+        assert err <= TOL[dtype]
+
+
+# -- BLAS edge semantics ------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_beta_zero_ignores_nan_in_c(cuda, dtype):
+    A, lda, B, ldb, C, ldc = make_inputs(dtype, 0, 0, 0, 300, 300, 64, SEED + 50)
+    C[:] = np.nan
+    got = run_sbx(cuda, dtype, 0, 0, 0, 300, 300, 64, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+    assert not np.isnan(got).any()
+    want = run_oracle(0, 0, 0, 300, 300, 64, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+    assert normwise(0, got, want, 300, 300, ldc) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_alpha_zero_and_k_zero_scale_c(cuda, dtype):
+    A, lda, B, ldb, C, ldc = make_inputs(dtype, 0, 0, 0, 70, 90, 33, SEED + 51)
+    A[:] = np.nan  # alpha == 0: A and B are not read
+    got = run_sbx(cuda, dtype, 0, 0, 0, 70, 90, 33, 0.0, A, lda, B, ldb, 2.0, C, ldc)
+    np.testing.assert_array_equal(got, (2.0 * C).astype(dtype))
+    got = run_sbx(cuda, dtype, 0, 0, 0, 70, 90, 0, 1.0, A, lda, B, ldb, -0.5, C, ldc)
+    np.testing.assert_array_equal(got, (-0.5 * C).astype(dtype))
+    Cn = C.copy()
+    Cn[:] = np.nan
+    got = run_sbx(cuda, dtype, 0, 0, 0, 70, 90, 0, 1.0, A, lda, B, ldb, 0.0, Cn, ldc)
+    assert (got == 0).all()
+
+
+def test_empty_m_or_n_is_noop(cuda):
+    A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, 4, 4, 4, SEED + 52)
+    got = run_sbx(cuda, np.float32, 0, 0, 0, 0, 4, 4, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+    np.testing.assert_array_equal(got, C)
+    got = run_sbx(cuda, np.float32, 0, 0, 0, 4, 0, 4, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+    np.testing.assert_array_equal(got, C)
+
+
+# -- strided batched (gemm.cpp:55-58, :68-72) ---------------------------------
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_strided_batched(cuda, dtype, layout):
+    import torch
+    import sushiblas_amd as sbx
+    batch, m, n, k = 5, 97, 130, 71
+    ta, tb = 1, 0
+    sa = (k, m) if ta else (m, k)
+    sb = (n, k) if tb else (k, n)
+    lda = sa[1] if layout == 0 else sa[0]
+    ldb = sb[1] if layout == 0 else sb[0]
+    ldc = n if layout == 0 else m
+    str_a, str_b, str_c = sa[0] * sa[1] + 3, sb[0] * sb[1] + 1, m * n + 2
+    A = oracle.fill_uniform(batch * str_a, dtype, SEED + 60, 0)
+    B = oracle.fill_uniform(batch * str_b, dtype, SEED + 60, 1)
+    C = oracle.fill_uniform(batch * str_c, dtype, SEED + 60, 2)
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
+    sbx.gemm_ex(sbx.F32 if dtype == np.float32 else sbx.F64, layout, ta, tb, m, n, k, 0.5, dA,
+                lda, str_a, dB, ldb, str_b, 1.5, dC, ldc, str_c, batch)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    want = C.copy()
+    oracle.gemm_strided_batched(layout, ta, tb, m, n, k, 0.5, A, lda, str_a, B, ldb, str_b, 1.5,
+                                want, ldc, str_c, batch, 1)
+    for b in range(batch):
+        g = c_window(layout, got[b * str_c:b * str_c + m * n], m, n, ldc)
+        w = c_window(layout, want[b * str_c:b * str_c + m * n], m, n, ldc)
+        assert oracle.rel_fro_err(g, w) <= TOL[dtype]
+    # padding between batch entries is untouched
+    for b in range(batch):
+        np.testing.assert_array_equal(got[b * str_c + m * n:(b + 1) * str_c],
+                                      C[b * str_c + m * n:(b + 1) * str_c])
+    del tdt
+
+
+def test_batched_broadcast_b(cuda):
+    """str_b = 0: every batch entry multiplies by the same B."""
+    import torch
+    import sushiblas_amd as sbx
+    batch, m, n, k = 4, 64, 96, 48
+    A = oracle.fill_uniform(batch * m * k, np.float32, SEED + 61, 0)
+    B = oracle.fill_uniform(k * n, np.float32, SEED + 61, 1)
+    C = np.zeros(batch * m * n, np.float32)
+    dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
+    sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, dA, k, m * k, dB, n, 0, 0.0, dC, n, m * n, batch)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    for b in range(batch):
+        want = np.zeros(m * n, np.float32)
+        oracle.gemm(0, 0, 0, m, n, k, 1.0, A[b * m * k:(b + 1) * m * k], k, B, n, 0.0, want, n, 1)
+        assert oracle.rel_fro_err(got[b * m * n:(b + 1) * m * n].reshape(m, n),
+                                  want.reshape(m, n)) <= 1e-5
+
+
+# -- closed forms from the reference's integration tests ----------------------
+
+def test_parallel_batched_inference_closed_form(cuda):
+    """test_framework_sim.cpp:75-128: X = 1 (256x256), W = 2 (256x512) -> Y = 512,
+    24 independent models (run here as one strided batch)."""
+    import torch
+    import sushiblas_amd as sbx
+    models, m, n, k = 24, 256, 512, 256
+    X = torch.ones(models, m, k, device=cuda)
+    W = torch.full((models, k, n), 2.0, device=cuda)
+    Y = torch.empty(models, m, n, device=cuda)
+    sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, X, k, m * k, W, n, k * n, 0.0, Y, n, m * n,
+                models)
+    torch.cuda.synchronize()
+    assert bool((Y == 512.0).all())
+
+
+def test_deep_forward_pass_closed_form(cuda):
+    """test_framework_sim.cpp:10-73: X = 1 (512x1024), W_i = 0.01 (1024x1024),
+    10 layers, ReLU between (identity on these positive values): every entry
+    of layer L is (1024 * fp32(0.01))^L up to fp32 rounding -- each layer sums
+    1024 products in fp32, a relative error of at most ~1024 * 2^-24 = 6e-5
+    per layer in the worst case."""
+    import torch
+    import sushiblas_amd as sbx
+    b, f = 512, 1024
+    H = torch.ones(b, f, device=cuda)
+    W = torch.full((f, f), 0.01, device=cuda)
+    for layer in range(1, 11):
+        Hn = torch.empty(b, f, device=cuda)
+        sbx.sgemm(0, 0, 0, b, f, f, 1.0, H, f, W, f, 0.0, Hn, f)
+        if layer < 10:
+            Hn = torch.relu(Hn)
+        H = Hn
+        torch.cuda.synchronize()
+        expect = (1024 * np.float64(np.float32(0.01))) ** layer
+        rel = float((H.double() - expect).abs().max() / expect)
+        assert rel < 6.2e-5 * layer, (layer, rel)
