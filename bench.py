@@ -43,7 +43,22 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (torch copy_) a few "
+                         "times: the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """1 GiB read + 1 GiB write per dispatch of torch's copy kernel."""
+    import torch
+    n = 1 << 28  # float32 elements = 1 GiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n * 4, "dispatches": 3}), flush=True)
 
 
 def time_launches(fn, steps, warmup):
@@ -160,6 +175,9 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     import numpy as np
     import torch
     import sushiblas_amd as sbx

@@ -1,0 +1,120 @@
+// level3_gemm.cpp -- Level3::gemm on the gfx950 backend.
+//
+// Same validation, parameter derivation and task recording as the reference
+// (src/ops/blas/level3/gemm.cpp:82-198): m, n, k, batch, leading dimensions
+// from the SHAPES, batch strides strides[r-3], layout taken from A, read and
+// write sets from the storage base pointers, the "blas.lvl3.gemm" metadata.
+// The recorded closure calls the C ABI (include/sbx.h) on the context's HIP
+// stream where the reference's gemm_dispatch<T> (gemm.cpp:44-79) calls oneMKL.
+#include <SushiBLAS/engine.hpp>
+#include <SushiBLAS/ops/blas/level3.hpp>
+
+#include "../../../include/sbx.h"
+
+namespace SushiBLAS
+{
+    using namespace SushiRuntime::Graph::Literals;
+    using SushiRuntime::Execution::Event;
+    using SushiRuntime::Execution::Queue;
+
+    namespace
+    {
+        const char* dtype_name(Core::DataType t)
+        {
+            switch (t)
+            {
+                case Core::DataType::HALF: return "HALF";
+                case Core::DataType::FLOAT32: return "FLOAT32";
+                case Core::DataType::FLOAT64: return "FLOAT64";
+                case Core::DataType::COMPLEX32: return "COMPLEX32";
+                case Core::DataType::COMPLEX64: return "COMPLEX64";
+            }
+            return "?";
+        }
+    } // namespace
+
+    Event Level3::gemm(const Tensor& A, const Tensor& B, Tensor& C, bool transA, bool transB,
+                       float alpha, float beta)
+    {
+        SB_THROW_IF(A.rank < 2 || B.rank < 2 || C.rank < 2, "GEMM requires at least 2D tensors.");
+        SB_THROW_IF(A.dtype != B.dtype || A.dtype != C.dtype, "Data type mismatch in GEMM operation.");
+
+        const int32_t rA = A.rank, rB = B.rank, rC = C.rank;
+        const int64_t m = C.shape[rC - 2];
+        const int64_t n = C.shape[rC - 1];
+        const int64_t k = transA ? A.shape[rA - 2] : A.shape[rA - 1];
+
+        int64_t batch_size = 1;
+        for (int i = 0; i < rC - 2; ++i) batch_size *= C.shape[i];
+
+        const int64_t lda = (A.layout == Core::Layout::ROW_MAJOR) ? A.shape[rA - 1] : A.shape[rA - 2];
+        const int64_t ldb = (B.layout == Core::Layout::ROW_MAJOR) ? B.shape[rB - 1] : B.shape[rB - 2];
+        const int64_t ldc = (C.layout == Core::Layout::ROW_MAJOR) ? C.shape[rC - 1] : C.shape[rC - 2];
+
+        const int64_t str_a = (batch_size > 1) ? A.strides[rA - 3] : 0;
+        const int64_t str_b = (batch_size > 1) ? B.strides[rB - 3] : 0;
+        const int64_t str_c = (batch_size > 1) ? C.strides[rC - 3] : 0;
+
+        const int layout = (A.layout == Core::Layout::ROW_MAJOR) ? 0 : 1;
+        const int tA = transA ? 1 : 0, tB = transB ? 1 : 0;
+
+        std::vector<void*> reads, writes;
+        if (A.storage && A.storage->data_ptr) reads.push_back(A.storage->data_ptr);
+        if (B.storage && B.storage->data_ptr) reads.push_back(B.storage->data_ptr);
+        if (C.storage && C.storage->data_ptr) writes.push_back(C.storage->data_ptr);
+
+        SushiRuntime::Graph::TaskMetadata meta;
+        meta.name = "blas.lvl3.gemm";
+        meta.task_type = SushiRuntime::Graph::TaskType::MATH_OP;
+        meta.op_id = "blas.lvl3.gemm"_op;
+        meta.set_param(0, alpha);
+        meta.set_param(1, beta);
+        meta.set_param(2, transA);
+        meta.set_param(3, transB);
+
+        auto& graph = engine_.get_graph();
+        switch (A.dtype)
+        {
+            case Core::DataType::FLOAT32:
+            {
+                graph.add_task(meta, reads, writes,
+                    [=, pA = A.device_data_as<float>(), pB = B.device_data_as<float>(),
+                     pC = C.device_data_as<float>()](Queue& q, const std::vector<Event>&) -> Event
+                    {
+                        const int st = sbx_sgemm_strided_batched(q.native(), layout, tA, tB, m, n, k,
+                                                                 alpha, pA, lda, str_a, pB, ldb, str_b,
+                                                                 beta, pC, ldc, str_c, batch_size);
+                        SB_THROW_IF(st != SBX_OK, "GEMM [{}x{}x{}, batch {}] failed: {}", m, n, k,
+                                    batch_size, sbx_status_string(st));
+                        return Event();
+                    });
+                break;
+            }
+            case Core::DataType::FLOAT64:
+            {
+                graph.add_task(meta, reads, writes,
+                    [=, alpha_d = static_cast<double>(alpha), beta_d = static_cast<double>(beta),
+                     pA = A.device_data_as<double>(), pB = B.device_data_as<double>(),
+                     pC = C.device_data_as<double>()](Queue& q, const std::vector<Event>&) -> Event
+                    {
+                        const int st = sbx_dgemm_strided_batched(q.native(), layout, tA, tB, m, n, k,
+                                                                 alpha_d, pA, lda, str_a, pB, ldb, str_b,
+                                                                 beta_d, pC, ldc, str_c, batch_size);
+                        SB_THROW_IF(st != SBX_OK, "GEMM [{}x{}x{}, batch {}] failed: {}", m, n, k,
+                                    batch_size, sbx_status_string(st));
+                        return Event();
+                    });
+                break;
+            }
+            case Core::DataType::HALF:
+            case Core::DataType::COMPLEX32:
+            case Core::DataType::COMPLEX64:
+                SB_THROW_IF(true, "GEMM on {} is not provided by the gfx950 backend "
+                                  "(FLOAT32 and FLOAT64 only).", dtype_name(A.dtype));
+                break;
+            default:
+                SB_THROW_IF(true, "Unsupported data type for GEMM operation.");
+        }
+        return Event();
+    }
+} // namespace SushiBLAS

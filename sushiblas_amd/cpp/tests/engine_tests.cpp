@@ -1,0 +1,555 @@
+// engine_tests.cpp -- tests of the C++ Engine/Tensor/Storage/Level3::gemm layer.
+//
+// The GEMM cases mirror the reference's own tests: tests/blas/level3/test_gemm.cpp
+// (known answers), tests/runtime/test_framework_sim.cpp (checked here by value
+// through closed forms, where the reference checks only shapes) and
+// tests/runtime/test_dependency_stress.cpp (same fan-out; values checked too).
+// GoogleTest is not available, so a minimal runner stands in: each case is
+// "cpu" (no device needed) or "gpu"; `--cpu`, `--gpu` or case names select.
+// Output: one "[  OK  ] name" or "[FAILED] name: reason" line per case; the
+// exit status is the number of failed cases.
+#include <SushiBLAS/SushiBLAS.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+namespace
+{
+    struct Failure
+    {
+        std::string what;
+    };
+
+    struct Case
+    {
+        const char* name;
+        bool gpu;
+        std::function<void()> fn;
+    };
+
+    std::vector<Case>& registry()
+    {
+        static std::vector<Case> r;
+        return r;
+    }
+
+    struct Register
+    {
+        Register(const char* name, bool gpu, std::function<void()> fn)
+        {
+            registry().push_back({name, gpu, std::move(fn)});
+        }
+    };
+
+#define TEST_CASE(name, gpu)                                  \
+    static void name();                                       \
+    static Register reg_##name(#name, gpu, name);             \
+    static void name()
+
+#define CHECK(cond)                                                                        \
+    do                                                                                     \
+    {                                                                                      \
+        if (!(cond))                                                                       \
+        {                                                                                  \
+            std::ostringstream os_;                                                        \
+            os_ << __FILE__ << ":" << __LINE__ << ": CHECK(" #cond ") failed";             \
+            throw Failure{os_.str()};                                                      \
+        }                                                                                  \
+    } while (0)
+
+#define CHECK_NEAR(a, b, tol)                                                              \
+    do                                                                                     \
+    {                                                                                      \
+        const double a_ = (a), b_ = (b);                                                   \
+        if (!(std::fabs(a_ - b_) <= (tol)))                                                \
+        {                                                                                  \
+            std::ostringstream os_;                                                        \
+            os_ << __FILE__ << ":" << __LINE__ << ": " #a " = " << a_ << " vs " #b " = " << b_; \
+            throw Failure{os_.str()};                                                      \
+        }                                                                                  \
+    } while (0)
+
+#define CHECK_THROWS(stmt)                                                                 \
+    do                                                                                     \
+    {                                                                                      \
+        bool thrown_ = false;                                                              \
+        try { stmt; } catch (const std::runtime_error&) { thrown_ = true; }                \
+        if (!thrown_) throw Failure{std::string(__FILE__) + ": expected a throw: " #stmt}; \
+    } while (0)
+
+    using sb::Core::DataType;
+    using sb::Core::Layout;
+    using sr::Memory::AllocStrategy;
+
+    // One device context per process, as the reference's fixture holds one
+    // static RuntimeContext (tests/test_common.hpp:15).
+    sr::Execution::RuntimeContext& ctx()
+    {
+        static sr::Execution::RuntimeContext c;
+        return c;
+    }
+
+    template <typename T = float>
+    void fill_tensor(sb::Tensor& t, const std::vector<T>& data)
+    {
+        CHECK(static_cast<int64_t>(data.size()) == t.num_elements);
+        std::memcpy(t.data_as<T>(), data.data(), data.size() * sizeof(T));
+    }
+
+    template <typename T = float>
+    void verify_tensor(const sb::Tensor& t, const std::vector<T>& expected, double abs_error = 1e-4)
+    {
+        CHECK(static_cast<int64_t>(expected.size()) == t.num_elements);
+        const T* p = t.data_as<T>();
+        for (size_t i = 0; i < expected.size(); ++i) CHECK_NEAR(p[i], expected[i], abs_error);
+    }
+} // namespace
+
+// ---------------------------------------------------------------- host only
+
+TEST_CASE(TensorStridesRowAndColumnMajor, false)
+{
+    sb::Tensor r(nullptr, {2, 3, 4});
+    CHECK(r.rank == 3 && r.num_elements == 24);
+    CHECK(r.strides[0] == 12 && r.strides[1] == 4 && r.strides[2] == 1);
+    sb::Tensor c(nullptr, {2, 3, 4}, 0, Layout::COLUMN_MAJOR);
+    CHECK(c.strides[0] == 1 && c.strides[1] == 2 && c.strides[2] == 6);
+    CHECK(r.is_contiguous() && c.is_contiguous());
+    CHECK(!r.transpose(0, 2).is_contiguous());
+    CHECK_THROWS(sb::Tensor(nullptr, {1, 1, 1, 1, 1, 1, 1}));
+}
+
+TEST_CASE(TensorViews, false)
+{
+    sb::Tensor t(nullptr, {4, 6});
+    sb::Tensor tt = t.transpose(0, 1);
+    CHECK(tt.shape[0] == 6 && tt.shape[1] == 4 && tt.strides[0] == 1 && tt.strides[1] == 6);
+    CHECK_THROWS(t.transpose(0, 2));
+    sb::Tensor s = t.slice(0, 1, -1);  // rows [1, 3)
+    CHECK(s.shape[0] == 2 && s.shape[1] == 6 && s.storage_offset == 6);
+    sb::Tensor s2 = t.slice(1, -100, 100);  // clamped
+    CHECK(s2.shape[1] == 6 && s2.storage_offset == 0);
+    t.dtype = DataType::FLOAT64;
+    sb::Tensor r = t.reshape({3, 8});
+    CHECK(r.shape[0] == 3 && r.shape[1] == 8 && r.dtype == DataType::FLOAT64);
+    CHECK_THROWS(t.reshape({5, 5}));
+    CHECK_THROWS(tt.reshape({24}));
+}
+
+TEST_CASE(OpIdIsFnv1a, false)
+{
+    using namespace sr::Graph::Literals;
+    CHECK(("blas.lvl3.gemm"_op).value == 0xaea52978u);
+    CHECK(sr::Graph::OpID::hash_str("", 0) == 2166136261u);
+    sr::Graph::TaskMetadata m;
+    m.set_param(0, 1.5f);
+    m.set_param(2, true);
+    CHECK(m.get_param<float>(0) == 1.5f && m.get_param<bool>(2));
+}
+
+TEST_CASE(ErrorFormatting, false)
+{
+    CHECK(sb::Core::format("a {} b {} c", 1, "x") == "a 1 b x c");
+    CHECK(sb::Core::format("no args") == "no args");
+    bool thrown = false;
+    try { SB_THROW_IF(true, "value {}", 42); }
+    catch (const std::runtime_error& e) { thrown = std::string(e.what()) == "value 42"; }
+    CHECK(thrown);
+}
+
+TEST_CASE(GemmValidationThrowsAtRecordTime, false)
+{
+    // An Engine over a context that has not touched the device yet: gemm()
+    // validates before it needs any allocation (gemm.cpp:87-88).
+    sr::Execution::RuntimeContext local;
+    sb::Engine e(local);
+    sb::Tensor a1(nullptr, {4});
+    sb::Tensor a2(nullptr, {4, 4});
+    sb::Tensor b2(nullptr, {4, 4});
+    sb::Tensor c2(nullptr, {4, 4});
+    CHECK_THROWS(e.blas().gemm(a1, b2, c2));
+    sb::Tensor d2(nullptr, {4, 4});
+    d2.dtype = DataType::FLOAT64;
+    CHECK_THROWS(e.blas().gemm(a2, d2, c2));
+    sb::Tensor h(nullptr, {4, 4});
+    h.dtype = DataType::HALF;
+    sb::Tensor h2 = h, h3 = h;
+    CHECK_THROWS(e.blas().gemm(h, h2, h3));       // not provided by this backend
+    CHECK_THROWS(e.blas().gemm(a2, b2, c2));      // no storage: data() throws at capture
+    CHECK(e.get_graph().pending() == 0);
+}
+
+TEST_CASE(SushiPtrRefCounting, false)
+{
+    struct Obj : sr::Core::RefCounted
+    {
+        int* alive;
+        explicit Obj(int* a) : alive(a) { ++*alive; }
+        ~Obj() override { --*alive; }
+    };
+    int alive = 0;
+    {
+        sr::sushi_ptr<Obj> a = sr::make_sushi<Obj>(&alive);
+        CHECK(alive == 1 && a->ref_count() == 1);
+        sr::sushi_ptr<Obj> b = a;
+        CHECK(a->ref_count() == 2);
+        b.reset();
+        CHECK(a->ref_count() == 1);
+    }
+    CHECK(alive == 0);
+}
+
+// ------------------------------------------------------------------ device
+
+TEST_CASE(SimpleGEMM3x3, true)  // tests/blas/level3/test_gemm.cpp:39-63
+{
+    sb::Engine engine(ctx(), Layout::ROW_MAJOR);
+    const int N = 3;
+    auto A = engine.create_tensor({N, N});
+    auto B = engine.create_tensor({N, N});
+    auto C = engine.create_tensor({N, N});
+    fill_tensor(A, {1, 2, 3, 4, 5, 6, 7, 8, 9});
+    fill_tensor(B, {2, 0, 0, 0, 2, 0, 0, 0, 2});
+    fill_tensor(C, std::vector<float>(N * N, 0.0f));
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    verify_tensor(C, {2, 4, 6, 8, 10, 12, 14, 16, 18});
+}
+
+TEST_CASE(SimpleGEMMColumnMajor, true)  // tests/blas/level3/test_gemm.cpp:65-88
+{
+    sb::Engine engine(ctx(), Layout::COLUMN_MAJOR);
+    auto A = engine.create_tensor({2, 2});
+    auto B = engine.create_tensor({2, 2});
+    auto C = engine.create_tensor({2, 2});
+    fill_tensor(A, {1, 3, 2, 4});
+    fill_tensor(B, {5, 7, 6, 8});
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    verify_tensor(C, {19, 43, 22, 50});
+}
+
+TEST_CASE(DeferredUntilExecute, true)
+{
+    sb::Engine engine(ctx());
+    auto A = engine.create_tensor({2, 2});
+    auto B = engine.create_tensor({2, 2});
+    auto C = engine.create_tensor({2, 2});
+    fill_tensor(A, {1, 2, 3, 4});
+    fill_tensor(B, {1, 0, 0, 1});
+    fill_tensor(C, {-1, -1, -1, -1});
+    sr::Execution::Event ev = engine.blas().gemm(A, B, C);
+    CHECK(ev.is_complete());                 // default event, as the reference returns
+    CHECK(engine.get_graph().pending() == 1);
+    ctx().wait_all();
+    verify_tensor(C, {-1, -1, -1, -1});       // nothing ran yet
+    engine.execute().wait();
+    verify_tensor(C, {1, 2, 3, 4});
+    CHECK(engine.get_graph().pending() == 0);
+}
+
+TEST_CASE(AlphaBetaTransposesFp32AndFp64, true)
+{
+    // op(A) = A^T with A stored 3x2 (k x m), op(B) = B^T with B stored 2x3 (n x k)
+    sb::Engine engine(ctx());
+    for (DataType dt : {DataType::FLOAT32, DataType::FLOAT64})
+    {
+        auto A = engine.create_tensor({3, 2}, dt);
+        auto B = engine.create_tensor({2, 3}, dt);
+        auto C = engine.create_tensor({2, 2}, dt);
+        const std::vector<double> a = {1, 2, 3, 4, 5, 6}, b = {1, 0, 2, 0, 1, 3}, c = {1, 1, 1, 1};
+        // op(A) = [[1,3,5],[2,4,6]], op(B) = [[1,0],[0,1],[2,3]] -> op(A)op(B) = [[11,18],[14,22]]
+        const std::vector<double> want = {2 * 11 - 1, 2 * 18 - 1, 2 * 14 - 1, 2 * 22 - 1};
+        if (dt == DataType::FLOAT32)
+        {
+            fill_tensor(A, std::vector<float>(a.begin(), a.end()));
+            fill_tensor(B, std::vector<float>(b.begin(), b.end()));
+            fill_tensor(C, std::vector<float>(c.begin(), c.end()));
+        }
+        else
+        {
+            fill_tensor(A, a);
+            fill_tensor(B, b);
+            fill_tensor(C, c);
+        }
+        engine.blas().gemm(A, B, C, true, true, 2.0f, -1.0f);
+        engine.execute().wait();
+        if (dt == DataType::FLOAT32) verify_tensor(C, std::vector<float>(want.begin(), want.end()));
+        else verify_tensor(C, want, 1e-12);
+    }
+}
+
+TEST_CASE(BatchedRank3, true)  // rank > 2 -> gemm_batch (gemm.cpp:55-58)
+{
+    sb::Engine engine(ctx());
+    const int batch = 4, m = 5, n = 3, k = 7;
+    auto A = engine.create_tensor({batch, m, k});
+    auto B = engine.create_tensor({batch, k, n});
+    auto C = engine.create_tensor({batch, m, n});
+    std::vector<float> a(batch * m * k), b(batch * k * n);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = float((i * 7) % 11) - 5.0f;
+    for (size_t i = 0; i < b.size(); ++i) b[i] = float((i * 5) % 13) - 6.0f;
+    fill_tensor(A, a);
+    fill_tensor(B, b);
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    std::vector<float> want(batch * m * n, 0.0f);
+    for (int z = 0; z < batch; ++z)
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j)
+            {
+                double s = 0;
+                for (int p = 0; p < k; ++p) s += a[z * m * k + i * k + p] * b[z * k * n + p * n + j];
+                want[z * m * n + i * n + j] = float(s);
+            }
+    verify_tensor(C, want);  // small integers: exact
+}
+
+TEST_CASE(SlicedOutputRows, true)
+{
+    // C is rows [2, 5) of a 6x4 tensor: the view's offset is applied to the
+    // device address, rows outside the slice stay untouched.
+    sb::Engine engine(ctx());
+    auto A = engine.create_tensor({3, 2});
+    auto B = engine.create_tensor({2, 4});
+    auto Cfull = engine.create_tensor({6, 4});
+    fill_tensor(A, {1, 2, 3, 4, 5, 6});
+    fill_tensor(B, {1, 0, 1, 0, 0, 1, 0, 1});
+    fill_tensor(Cfull, std::vector<float>(24, 9.0f));
+    sb::Tensor C = Cfull.slice(0, 2, 5);
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    std::vector<float> want(24, 9.0f);
+    const float rows[3][4] = {{1, 2, 1, 2}, {3, 4, 3, 4}, {5, 6, 5, 6}};
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 4; ++j) want[(i + 2) * 4 + j] = rows[i][j];
+    verify_tensor(Cfull, want);
+}
+
+TEST_CASE(DeviceStrategyWithExplicitStaging, true)
+{
+    sb::Engine engine(ctx());
+    const int n = 64;
+    auto A = engine.create_tensor({n, n}, DataType::FLOAT64, AllocStrategy::DEVICE);
+    auto B = engine.create_tensor({n, n}, DataType::FLOAT64, AllocStrategy::DEVICE);
+    auto C = engine.create_tensor({n, n}, DataType::FLOAT64, AllocStrategy::DEVICE);
+    std::vector<double> a(n * n), id(n * n, 0.0), c(n * n);
+    for (int i = 0; i < n * n; ++i) a[i] = 0.5 * (i % 17) - 3.0;
+    for (int i = 0; i < n; ++i) id[i * n + i] = 3.0;
+    A.storage->copy_from_host(a.data(), a.size() * sizeof(double));
+    B.storage->copy_from_host(id.data(), id.size() * sizeof(double));
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    C.storage->copy_to_host(c.data(), c.size() * sizeof(double));
+    for (int i = 0; i < n * n; ++i) CHECK(c[i] == 3.0 * a[i]);
+}
+
+TEST_CASE(HostStrategyPinnedMapped, true)
+{
+    sb::Engine engine(ctx());
+    auto A = engine.create_tensor({2, 2}, AllocStrategy::HOST);
+    auto B = engine.create_tensor({2, 2}, AllocStrategy::HOST);
+    auto C = engine.create_tensor({2, 2}, AllocStrategy::HOST);
+    fill_tensor(A, {1, 2, 3, 4});
+    fill_tensor(B, {0, 1, 1, 0});
+    engine.blas().gemm(A, B, C);
+    engine.execute().wait();
+    verify_tensor(C, {2, 1, 4, 3});
+}
+
+TEST_CASE(FrameworkSimDeepForwardPass, true)  // test_framework_sim.cpp:10-73
+{
+    sb::Engine engine(ctx());
+    const int batch_size = 512, features = 1024, num_layers = 10;
+    auto X = engine.create_tensor({batch_size, features});
+    fill_tensor(X, std::vector<float>(batch_size * features, 1.0f));
+    std::vector<sb::Tensor> weights, activations{X};
+    for (int i = 0; i < num_layers; ++i)
+    {
+        auto W = engine.create_tensor({features, features});
+        fill_tensor(W, std::vector<float>(features * features, 0.01f));
+        weights.push_back(W);
+        activations.push_back(engine.create_tensor({batch_size, features}));
+    }
+    // ReLU between layers is the identity on these positive values
+    for (int i = 0; i < num_layers; ++i) engine.blas().gemm(activations[i], weights[i], activations[i + 1]);
+    engine.execute().wait();
+    CHECK(activations.back().shape[0] == batch_size && activations.back().shape[1] == features);
+    for (int l = 1; l <= num_layers; ++l)
+    {
+        const double expect = std::pow(1024.0 * double(0.01f), l);
+        const float* p = activations[l].data_as<float>();
+        for (int i = 0; i < batch_size * features; i += 4099)
+            CHECK(std::fabs(p[i] - expect) <= 6.2e-5 * l * expect);
+    }
+}
+
+TEST_CASE(FrameworkSimParallelBatchedInference, true)  // test_framework_sim.cpp:75-128
+{
+    sb::Engine engine(ctx());
+    const int num_models = 24, m = 256, n = 512, k = 256;
+    std::vector<sb::Tensor> inputs, weights, outputs;
+    for (int i = 0; i < num_models; ++i)
+    {
+        auto X = engine.create_tensor({m, k});
+        fill_tensor(X, std::vector<float>(m * k, 1.0f));
+        inputs.push_back(X);
+        auto W = engine.create_tensor({k, n});
+        fill_tensor(W, std::vector<float>(k * n, 2.0f));
+        weights.push_back(W);
+        outputs.push_back(engine.create_tensor({m, n}));
+    }
+    for (int i = 0; i < num_models; ++i) engine.blas().gemm(inputs[i], weights[i], outputs[i]);
+    engine.execute().wait();
+    for (int i = 0; i < num_models; ++i)
+    {
+        CHECK(outputs[i].shape[0] == m && outputs[i].shape[1] == n);
+        verify_tensor(outputs[i], std::vector<float>(m * n, 512.0f), 0.0);
+    }
+}
+
+TEST_CASE(DependencyManyReadersOneWriter, true)  // test_dependency_stress.cpp:9-57
+{
+    sb::Engine engine(ctx());
+    const int num_readers = 5000, N = 32;
+    auto writer = engine.create_tensor({N, N});
+    fill_tensor(writer, std::vector<float>(N * N, 1.0f));
+    std::vector<sb::Tensor> outs;
+    for (int i = 0; i < num_readers; ++i)
+    {
+        auto t = engine.create_tensor({N, N});
+        fill_tensor(t, std::vector<float>(N * N, 0.0f));
+        outs.push_back(t);
+    }
+    auto w = engine.create_tensor({N, N});
+    fill_tensor(w, std::vector<float>(N * N, 2.0f));
+    engine.blas().gemm(w, w, writer);                   // writer = 2*2*32 = 128
+    for (int i = 0; i < num_readers; ++i) engine.blas().gemm(writer, w, outs[i]);  // 128*2*32
+    engine.execute().wait();
+    verify_tensor(writer, std::vector<float>(N * N, 128.0f), 0.0);
+    for (int i = 0; i < num_readers; i += 499) verify_tensor(outs[i], std::vector<float>(N * N, 8192.0f), 0.0);
+    verify_tensor(outs.back(), std::vector<float>(N * N, 8192.0f), 0.0);
+}
+
+TEST_CASE(DependencyShardCollision, true)  // test_dependency_stress.cpp:59-95
+{
+    sb::Engine engine(ctx());
+    const int num_ops = 3000, N = 8;
+    std::vector<sb::Tensor> As, Bs, Cs;
+    for (int i = 0; i < num_ops; ++i)
+    {
+        As.push_back(engine.create_tensor({N, N}));
+        Bs.push_back(engine.create_tensor({N, N}));
+        Cs.push_back(engine.create_tensor({N, N}));
+        fill_tensor(As.back(), std::vector<float>(N * N, float(i % 7)));
+        fill_tensor(Bs.back(), std::vector<float>(N * N, 1.0f));
+    }
+    for (int i = 0; i < num_ops; ++i) engine.blas().gemm(As[i], Bs[i], Cs[i]);
+    engine.execute().wait();
+    for (int i = 0; i < num_ops; i += 97) verify_tensor(Cs[i], std::vector<float>(N * N, 8.0f * (i % 7)), 0.0);
+}
+
+TEST_CASE(TraceHookSeesGemmMetadata, true)
+{
+    sb::Engine engine(ctx());
+    std::vector<std::string> names;
+    float alpha_seen = 0;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) {
+        names.push_back(m.name);
+        alpha_seen = m.get_param<float>(0);
+    });
+    auto A = engine.create_tensor({4, 4});
+    auto B = engine.create_tensor({4, 4});
+    auto C = engine.create_tensor({4, 4});
+    fill_tensor(A, std::vector<float>(16, 1.0f));
+    fill_tensor(B, std::vector<float>(16, 1.0f));
+    engine.blas().gemm(A, B, C, false, false, 0.5f, 0.0f);
+    engine.execute().wait();
+    CHECK(names.size() == 1 && names[0] == "blas.lvl3.gemm" && alpha_seen == 0.5f);
+    verify_tensor(C, std::vector<float>(16, 2.0f), 0.0);
+}
+
+TEST_CASE(LargeFp32MatchesHostLoop, true)
+{
+    // 300 x 257 x 129 with odd leading dimensions, against a double host loop
+    sb::Engine engine(ctx());
+    const int m = 300, n = 257, k = 129;
+    auto A = engine.create_tensor({m, k});
+    auto B = engine.create_tensor({k, n});
+    auto C = engine.create_tensor({m, n});
+    std::vector<float> a(m * k), b(k * n), c(m * n);
+    for (int i = 0; i < m * k; ++i) a[i] = std::sin(0.37f * i);
+    for (int i = 0; i < k * n; ++i) b[i] = std::cos(0.11f * i);
+    for (int i = 0; i < m * n; ++i) c[i] = 0.25f * ((i % 9) - 4);
+    fill_tensor(A, a);
+    fill_tensor(B, b);
+    fill_tensor(C, c);
+    engine.blas().gemm(A, B, C, false, false, 1.25f, 0.5f);
+    engine.execute().wait();
+    double num = 0, den = 0;
+    const float* got = C.data_as<float>();
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j)
+        {
+            double s = 0;
+            for (int p = 0; p < k; ++p) s += double(a[i * k + p]) * b[p * n + j];
+            const double want = 1.25 * s + 0.5 * c[i * n + j];
+            num += (got[i * n + j] - want) * (got[i * n + j] - want);
+            den += want * want;
+        }
+    CHECK(std::sqrt(num / den) <= 1e-5);
+}
+
+int main(int argc, char** argv)
+{
+    bool want_cpu = false, want_gpu = false, list = false;
+    std::vector<std::string> names;
+    for (int i = 1; i < argc; ++i)
+    {
+        std::string a = argv[i];
+        if (a == "--cpu") want_cpu = true;
+        else if (a == "--gpu") want_gpu = true;
+        else if (a == "--list") list = true;
+        else names.push_back(a);
+    }
+    if (!want_cpu && !want_gpu && names.empty()) want_cpu = want_gpu = true;
+    int failed = 0, ran = 0;
+    for (const Case& c : registry())
+    {
+        bool sel = (c.gpu ? want_gpu : want_cpu);
+        for (const auto& n : names) sel = sel || n == c.name;
+        if (!sel) continue;
+        if (list)
+        {
+            std::printf("%s %s\n", c.gpu ? "gpu" : "cpu", c.name);
+            continue;
+        }
+        ++ran;
+        std::printf("[ RUN  ] %s\n", c.name);
+        std::fflush(stdout);
+        try
+        {
+            c.fn();
+            std::printf("[  OK  ] %s\n", c.name);
+        }
+        catch (const Failure& f)
+        {
+            ++failed;
+            std::printf("[FAILED] %s: %s\n", c.name, f.what.c_str());
+        }
+        catch (const std::exception& e)
+        {
+            ++failed;
+            std::printf("[FAILED] %s: exception: %s\n", c.name, e.what());
+        }
+        std::fflush(stdout);
+    }
+    if (!list) std::printf("%d cases, %d failed\n", ran, failed);
+    return failed;
+}
