@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace sbx {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -172,6 +174,7 @@ struct GemmArgs {
     T alpha, beta;
     int tiles_m, tiles_n;
     int group_m;
+    bool c_vec;  // C rows allow 16-byte vector access (ldc, base and batch stride aligned)
 };
 
 // ---------------------------------------------------------------------------
@@ -180,7 +183,7 @@ struct GemmArgs {
 //   X : tile extent along m (for A) or n (for B).
 //   VEC: elements per global load (1, or 16 bytes / sizeof(T)).
 // ---------------------------------------------------------------------------
-template <typename T, int X, int BK, bool KC, int VEC>
+template <typename T, int X, int BK, bool KC, int VEC, int PF>
 struct Operand {
     static constexpr int V = 16 / (int)sizeof(T);
     static constexpr int PAD = KC ? V : 0;
@@ -196,7 +199,7 @@ struct Operand {
     int lds_off[NV];   // element offset in the LDS tile
     int kidx[NV];      // k index of each vector within the tile
     bool xok[NV];      // row/column validity along X (fixed for the block)
-    raw_t stage[NV];
+    raw_t stage[PF][NV];  // register staging, PF tiles in flight
 
     __device__ inline void init(int tid, int64_t ld, int x_rem)
     {
@@ -217,19 +220,21 @@ struct Operand {
         }
     }
 
+    template <int S>
     __device__ inline void load(__amdgpu_buffer_rsrc_t rs, int k_rem)
     {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             bool ok = xok[j] && kidx[j] < k_rem;
-            stage[j] = Raw<VEC * sizeof(T)>::load(rs, ok ? off[j] : kOobOffset);
+            stage[S][j] = Raw<VEC * sizeof(T)>::load(rs, ok ? off[j] : kOobOffset);
         }
     }
 
+    template <int S>
     __device__ inline void store(T* lds)
     {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) *reinterpret_cast<raw_t*>(lds + lds_off[j]) = stage[j];
+        for (int j = 0; j < NV; ++j) *reinterpret_cast<raw_t*>(lds + lds_off[j]) = stage[S][j];
     }
 };
 
@@ -270,26 +275,86 @@ struct Frag {
     }
 };
 
+// Typed vector store/load of U consecutive C elements (16 bytes for fp32 U=4).
+template <typename T, int U>
+struct CVec {
+    __device__ static inline void load(const T* p, T* o)
+    {
+#pragma unroll
+        for (int u = 0; u < U; ++u) o[u] = p[u];
+    }
+    __device__ static inline void store(T* p, const T* v)
+    {
+#pragma unroll
+        for (int u = 0; u < U; ++u) p[u] = v[u];
+    }
+};
+template <>
+struct CVec<float, 4> {
+    __device__ static inline void load(const float* p, float* o)
+    {
+        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static inline void store(float* p, const float* v)
+    {
+        f32x4 w = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(p) = w;
+    }
+};
+template <>
+struct CVec<float, 2> {
+    __device__ static inline void load(const float* p, float* o)
+    {
+        f32x2 v = *reinterpret_cast<const f32x2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    }
+    __device__ static inline void store(float* p, const float* v)
+    {
+        f32x2 w = {v[0], v[1]};
+        *reinterpret_cast<f32x2*>(p) = w;
+    }
+};
+template <>
+struct CVec<double, 2> {
+    __device__ static inline void load(const double* p, double* o)
+    {
+        f64x2 v = *reinterpret_cast<const f64x2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    }
+    __device__ static inline void store(double* p, const double* v)
+    {
+        f64x2 w = {v[0], v[1]};
+        *reinterpret_cast<f64x2*>(p) = w;
+    }
+};
+
+template <int N>
+using Int = std::integral_constant<int, N>;
+
+// PF: global tiles in flight (1 = the next tile is fetched while the current
+// one is multiplied; 2 = the one after that too, for HBM-bound shapes).
+// WPE: waves per SIMD the register budget is sized for (1 or 2).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          int VA, int VB>
-__global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(GemmArgs<T> p)
+          int VA, int VB, int PF, int WPE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_mfma_kernel(GemmArgs<T> p)
 {
     typedef Mfma<T> MF;
     constexpr int MB = MF::MB;
     constexpr int V = MF::V;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int NBM = WTM / MB, NBN = WTN / MB;
+    constexpr int G = BK / 8;  // k groups per tile
     static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
     static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
-    typedef Operand<T, BM, BK, A_KC, VA> OpA;
-    typedef Operand<T, BN, BK, B_KC, VB> OpB;
+    static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
+    typedef Operand<T, BM, BK, A_KC, VA, PF> OpA;
+    typedef Operand<T, BN, BK, B_KC, VB, PF> OpB;
     typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
     typedef Frag<T, NBN, B_KC, OpB::LD> FragB;
 
     __shared__ __attribute__((aligned(16))) T smem[2 * (OpA::ELEMS + OpB::ELEMS)];
-    // buffer b of A at smem + b*ELEMS_A, of B at smem + 2*ELEMS_A + b*ELEMS_B
-    auto lds_a = [&](int b) { return smem + b * OpA::ELEMS; };
-    auto lds_b = [&](int b) { return smem + 2 * OpA::ELEMS + b * OpB::ELEMS; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -324,8 +389,8 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(GemmArgs<T> p)
                                 : ((int64_t)(p.K - 1) * p.lda + p.M) * (int64_t)sizeof(T);
     const int64_t b_span = B_KC ? ((int64_t)(p.N - 1) * p.ldb + p.K) * (int64_t)sizeof(T)
                                 : ((int64_t)(p.K - 1) * p.ldb + p.N) * (int64_t)sizeof(T);
-    int64_t a_pos = A_KC ? (int64_t)m0 * p.lda : (int64_t)m0;  // element offset of tile origin
-    int64_t b_pos = B_KC ? (int64_t)n0 * p.ldb : (int64_t)n0;
+    const int64_t a_org = A_KC ? (int64_t)m0 * p.lda : (int64_t)m0;  // element offset, tile 0
+    const int64_t b_org = B_KC ? (int64_t)n0 * p.ldb : (int64_t)n0;
     const int64_t a_step = A_KC ? BK : (int64_t)BK * p.lda;
     const int64_t b_step = B_KC ? BK : (int64_t)BK * p.ldb;
 
@@ -344,57 +409,161 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(GemmArgs<T> p)
 
     const int nk = (p.K + BK - 1) / BK;
 
-    opa.load(make_rsrc(A + a_pos, a_span - a_pos * (int64_t)sizeof(T)), p.K);
-    opb.load(make_rsrc(B + b_pos, b_span - b_pos * (int64_t)sizeof(T)), p.K);
-    opa.store(lds_a(0));
-    opb.store(lds_b(0));
-    __syncthreads();
+    // global tile kt -> staging set S
+    auto issue = [&](auto S, int kt) {
+        const int64_t pa = a_org + kt * a_step, pb = b_org + kt * b_step;
+        const int k_rem = p.K - kt * BK;
+        opa.template load<decltype(S)::value>(
+            make_rsrc(A + pa, a_span - pa * (int64_t)sizeof(T)), k_rem);
+        opb.template load<decltype(S)::value>(
+            make_rsrc(B + pb, b_span - pb * (int64_t)sizeof(T)), k_rem);
+    };
+    // staging set S -> LDS buffer buf
+    auto commit = [&](auto S, int buf) {
+        opa.template store<decltype(S)::value>(smem + buf * OpA::ELEMS);
+        opb.template store<decltype(S)::value>(smem + 2 * OpA::ELEMS + buf * OpB::ELEMS);
+    };
 
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
+    T fa[2][NBM][V], fb[2][NBN][V];  // fragments, double-buffered across k groups
+    auto read_frags = [&](auto F, int buf, int g) {
+        FragA::read(smem + buf * OpA::ELEMS, wm0, g, lane, fa[decltype(F)::value]);
+        FragB::read(smem + 2 * OpA::ELEMS + buf * OpB::ELEMS, wn0, g, lane,
+                    fb[decltype(F)::value]);
+    };
+    auto mma = [&](auto F) {
+        constexpr int f = decltype(F)::value;
+#pragma unroll
+        for (int kk = 0; kk < V; ++kk)
+#pragma unroll
+            for (int i = 0; i < NBM; ++i)
+#pragma unroll
+                for (int j = 0; j < NBN; ++j) acc[i][j] = MF::mma(fa[f][i][kk], fb[f][j][kk], acc[i][j]);
+    };
+
+    // Instruction counts that the scheduling hints below interleave.
+    constexpr int MPG = NBM * NBN * V;  // MFMAs per k group
+    constexpr int RPG = (A_KC ? NBM : NBM / FragA::U * V) + (B_KC ? NBN : NBN / FragB::U * V);
+    constexpr int NLD = OpA::NV + OpB::NV;  // global loads (= LDS writes) per tile
+    static_assert(G % 2 == 0, "fragment double-buffering needs an even number of k groups");
+
+    // One k tile held in LDS buffer cur (= kt & 1), its group-0 fragments
+    // already in registers.  Region A: the MFMAs of groups 0..G-2 overlap the
+    // next tile's global loads, the fragment reads of groups 1..G-1 and the
+    // LDS writes of the next tile.  Then one barrier.  Region B: the MFMAs of
+    // the last group overlap the fragment reads of the next tile's group 0.
+    // With PF == 2, staging set S holds tile kt + 1 on entry and set S ^ 1
+    // receives tile kt + 2, so the LDS writes never wait on fresh loads.
+    auto step = [&](auto S, int kt, int cur) {
+        constexpr int st = decltype(S)::value;
         const bool more = kt + 1 < nk;
-        if (more) {
-            a_pos += a_step;
-            b_pos += b_step;
-            const int k_rem = p.K - (kt + 1) * BK;
-            opa.load(make_rsrc(A + a_pos, a_span - a_pos * (int64_t)sizeof(T)), k_rem);
-            opb.load(make_rsrc(B + b_pos, b_span - b_pos * (int64_t)sizeof(T)), k_rem);
+        if (PF == 1) {
+            if (more) issue(Int<0>{}, kt + 1);
+        } else {
+            if (kt + 2 < nk) issue(Int<st ^ 1>{}, kt + 2);
         }
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
-            T fa[NBM][V], fb[NBN][V];
-            FragA::read(lds_a(cur), wm0, g, lane, fa);
-            FragB::read(lds_b(cur), wn0, g, lane, fb);
-#pragma unroll
-            for (int kk = 0; kk < V; ++kk)
-#pragma unroll
-                for (int i = 0; i < NBM; ++i)
-#pragma unroll
-                    for (int j = 0; j < NBN; ++j) acc[i][j] = MF::mma(fa[i][kk], fb[j][kk], acc[i][j]);
+        for (int g = 0; g + 1 < G; ++g) {
+            if (((g + 1) & 1) == 0) read_frags(Int<0>{}, cur, g + 1);
+            else read_frags(Int<1>{}, cur, g + 1);
+            if ((g & 1) == 0) mma(Int<0>{});
+            else mma(Int<1>{});
         }
-        if (more) {
-            opa.store(lds_a(cur ^ 1));
-            opb.store(lds_b(cur ^ 1));
+        if (more) commit(Int<PF == 1 ? 0 : st>{}, cur ^ 1);
+        // region A: loads first, then fragment reads, then the LDS writes,
+        // each memory instruction followed by a slice of the MFMAs
+        {
+            constexpr int mf = (G - 1) * MPG;
+            constexpr int mem = NLD + (G - 1) * RPG + NLD;
+            constexpr int per = mf / mem > 0 ? mf / mem : 1;
+#pragma unroll
+            for (int x = 0; x < NLD; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);  // MFMA
+            }
+#pragma unroll
+            for (int x = 0; x < (G - 1) * RPG; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
+            }
+#pragma unroll
+            for (int x = 0; x < NLD; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, mf, 0);
         }
         __syncthreads();
+        if (more) read_frags(Int<0>{}, cur ^ 1, 0);
+        mma(Int<1>{});
+        // region B: the next tile's group-0 reads spread over the last group
+        {
+            constexpr int per = MPG / RPG > 0 ? MPG / RPG : 1;
+#pragma unroll
+            for (int x = 0; x < RPG; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x008, per, 1);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, MPG, 1);
+        }
+    };
+
+    // prologue: tile 0 -> LDS buffer 0 (and tile 1 -> staging set 0 if PF == 2)
+    if (PF == 1) {
+        issue(Int<0>{}, 0);
+        commit(Int<0>{}, 0);
+    } else {
+        issue(Int<PF - 1>{}, 0);
+        commit(Int<PF - 1>{}, 0);
+        if (nk > 1) issue(Int<0>{}, 1);
+    }
+    __syncthreads();
+    read_frags(Int<0>{}, 0, 0);
+
+    if (PF == 1) {
+        for (int kt = 0; kt < nk; ++kt) step(Int<0>{}, kt, kt & 1);
+    } else {
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(Int<0>{}, kt, 0);
+            if (kt + 1 < nk) step(Int<1>{}, kt + 1, 1);
+        }
     }
 
     // ---- epilogue: C = alpha*acc + beta*C (C is not read when beta == 0) ----
+    // With B n-contiguous, a lane owns UB consecutive columns of each row and
+    // writes them with one vector store when C allows it.
+    constexpr int UB = FragB::U;
     const int q = lane / MB, jl = lane % MB;
     const bool read_c = p.beta != (T)0;
 #pragma unroll
     for (int i = 0; i < NBM; ++i)
 #pragma unroll
-        for (int j = 0; j < NBN; ++j) {
-            const int n = n0 + wn0 + FragB::map(j, jl);
+        for (int s = 0; s < NBN / UB; ++s) {
+            const int nb = n0 + wn0 + FragB::map(s * UB, jl);
+            const bool vec = UB > 1 && p.c_vec && nb + UB <= p.N;
 #pragma unroll
             for (int r = 0; r < MF::NACC; ++r) {
                 const int m = m0 + wm0 + FragA::map(i, MF::row(r, q));
-                if (m < p.M && n < p.N) {
-                    T* cp = C + (int64_t)m * p.ldc + n;
-                    T v = p.alpha * acc[i][j][r];
-                    if (read_c) v += p.beta * *cp;
-                    *cp = v;
+                if (m >= p.M) continue;
+                T* cp = C + (int64_t)m * p.ldc + nb;
+                T v[UB];
+#pragma unroll
+                for (int u = 0; u < UB; ++u) v[u] = p.alpha * acc[i][s * UB + u][r];
+                if (vec) {
+                    if (read_c) {
+                        T c[UB];
+                        CVec<T, UB>::load(cp, c);
+#pragma unroll
+                        for (int u = 0; u < UB; ++u) v[u] += p.beta * c[u];
+                    }
+                    CVec<T, UB>::store(cp, v);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < UB; ++u)
+                        if (nb + u < p.N) {
+                            T w = v[u];
+                            if (read_c) w += p.beta * cp[u];
+                            cp[u] = w;
+                        }
                 }
             }
         }

@@ -11,7 +11,7 @@
 
 namespace sbx {
 
-template <typename T, int BM, int BN, int BK, int WM, int WN>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, bool b_vec,
                        int batch, hipStream_t stream);
 
@@ -26,18 +26,19 @@ hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, 
                         int batch, hipStream_t stream);
 
 // Tile configurations compiled into the library, one translation unit each
-// (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp).
-#define SBX_MFMA_CONFIGS(X)            \
-    X(float, 256, 256, 16, 2, 2)       \
-    X(float, 128, 128, 16, 2, 2)       \
-    X(float, 256, 64, 16, 4, 1)        \
-    X(float, 64, 256, 16, 1, 4)        \
-    X(double, 128, 128, 16, 2, 2)      \
-    X(double, 256, 64, 16, 4, 1)       \
-    X(double, 64, 256, 16, 1, 4)
+// (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp):
+// (T, BM, BN, BK, waves along M, waves along N, prefetch depth, waves/SIMD)
+#define SBX_MFMA_CONFIGS(X)  \
+    X(float, 256, 256, 16, 2, 2, 1, 1) \
+    X(float, 128, 128, 16, 2, 2, 2, 2) \
+    X(float, 128, 64, 32, 2, 2, 2, 2) \
+    X(float, 64, 128, 32, 2, 2, 2, 2) \
+    X(double, 128, 128, 16, 2, 2, 1, 2) \
+    X(double, 128, 64, 16, 2, 2, 2, 2) \
+    X(double, 64, 128, 16, 2, 2, 2, 2)
 
-#define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN)                                                  \
-    extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN>(                                \
+#define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN, PF, WPE)                                        \
+    extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN, PF, WPE>(                         \
         const GemmArgs<T>&, bool, bool, bool, bool, int, hipStream_t);
 SBX_MFMA_CONFIGS(SBX_EXTERN_LAUNCH)
 #undef SBX_EXTERN_LAUNCH

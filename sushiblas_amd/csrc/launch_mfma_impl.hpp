@@ -8,7 +8,7 @@
 
 namespace sbx {
 
-template <typename T, int BM, int BN, int BK, int WM, int WN>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, bool b_vec,
                        int batch, hipStream_t stream)
 {
@@ -17,7 +17,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, b
     const dim3 block(256);
     const int sel = (a_kc ? 8 : 0) | (b_kc ? 4 : 0) | (a_vec ? 2 : 0) | (b_vec ? 1 : 0);
 #define SBX_LAUNCH(AK, BKC, VA, VB) \
-    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, VA, VB><<<grid, block, 0, stream>>>(a)
+    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, VA, VB, PF, WPE><<<grid, block, 0, stream>>>(a)
     switch (sel) {
     case 0: SBX_LAUNCH(false, false, 1, 1); break;
     case 1: SBX_LAUNCH(false, false, 1, V); break;

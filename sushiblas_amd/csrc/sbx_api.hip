@@ -39,13 +39,13 @@ struct Problem {
 
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
 enum Cfg {
-    F32_256x256,   // square/large fp32: 4 waves of 128x128
-    F32_128x128,   // mid-size fp32: 4 waves of 64x64
-    F32_256x64,    // n <= 64 (tall-skinny): 4 waves stacked along m
-    F32_64x256,    // m <= 64
-    F64_128x128,   // fp64: 4 waves of 64x64
-    F64_256x64,
-    F64_64x256,
+    F32_256x256,   // large fp32: 4 waves of 128x128, 1 wave/SIMD (256 accumulators)
+    F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
+    F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
+    F32_64x128,    // m <= 64
+    F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
+    F64_128x64,
+    F64_64x128,
     GENERIC,
 };
 
@@ -56,9 +56,9 @@ struct CfgInfo {
 
 const CfgInfo kCfg[] = {
     {"mfma_f32_256x256x16_w2x2", 256, 256, 16}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16},
-    {"mfma_f32_256x64x16_w4x1", 256, 64, 16},   {"mfma_f32_64x256x16_w1x4", 64, 256, 16},
-    {"mfma_f64_128x128x16_w2x2", 128, 128, 16}, {"mfma_f64_256x64x16_w4x1", 256, 64, 16},
-    {"mfma_f64_64x256x16_w1x4", 64, 256, 16},   {"generic_64x64x16", 64, 64, 16},
+    {"mfma_f32_128x64x32_w2x2", 128, 64, 32},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32},
+    {"mfma_f64_128x128x16_w2x2", 128, 128, 16}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16},
+    {"mfma_f64_64x128x16_w2x2", 64, 128, 16},   {"generic_64x64x16", 64, 64, 16},
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -66,13 +66,13 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 Cfg choose_cfg(int dtype, int64_t m, int64_t n)
 {
     if (dtype == SBX_F32) {
-        if (n <= 64) return F32_256x64;
-        if (m <= 64) return F32_64x256;
+        if (n <= 64) return F32_128x64;
+        if (m <= 64) return F32_64x128;
         if (cdiv(m, 256) * cdiv(n, 256) >= 256) return F32_256x256;
         return F32_128x128;
     }
-    if (n <= 64) return F64_256x64;
-    if (m <= 64) return F64_64x256;
+    if (n <= 64) return F64_128x64;
+    if (m <= 64) return F64_64x128;
     return F64_128x128;
 }
 
@@ -123,13 +123,13 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan p
 {
     switch (cfg) {
     case F32_256x256:
-        return launch_mfma<float, 256, 256, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 256, 256, 16, 2, 2, 1, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_128x128:
-        return launch_mfma<float, 128, 128, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
-    case F32_256x64:
-        return launch_mfma<float, 256, 64, 16, 4, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
-    case F32_64x256:
-        return launch_mfma<float, 64, 256, 16, 1, 4>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_128x64:
+        return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_64x128:
+        return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -142,11 +142,11 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, OperandPlan pa, OperandPlan 
 {
     switch (cfg) {
     case F64_128x128:
-        return launch_mfma<double, 128, 128, 16, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
-    case F64_256x64:
-        return launch_mfma<double, 256, 64, 16, 4, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
-    case F64_64x256:
-        return launch_mfma<double, 64, 256, 16, 1, 4>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<double, 128, 128, 16, 2, 2, 1, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F64_128x64:
+        return launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F64_64x128:
+        return launch_mfma<double, 64, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -187,6 +187,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.tiles_m = (int)cdiv(p.m, ci.bm);
             a.tiles_n = (int)cdiv(p.n, ci.bn);
             a.group_m = a.tiles_m < 8 ? a.tiles_m : 8;
+            a.c_vec = p.ldc % (16 / (int64_t)sizeof(T)) == 0 && (uintptr_t)a.C % 16 == 0 &&
+                      (p.batch <= 1 || p.str_c % (16 / (int64_t)sizeof(T)) == 0);
             const size_t elem = sizeof(T);
             const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
                                                 a.A, elem);

@@ -85,11 +85,11 @@ def test_noop_cases_need_no_device():
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x16_w2x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2"),
-    (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_256x64x16_w4x1"),
-    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x256x16_w1x4"),
-    (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_256x64x16_w4x1"),
+    (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
+    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x128x32_w2x2"),
+    (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
-    (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_256x64x16_w4x1"),
+    (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
 ])
 def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     sa = (k, m) if ta else (m, k)
