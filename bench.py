@@ -78,15 +78,17 @@ def time_launches(fn, steps, warmup):
     return start.elapsed_time(end) / steps  # ms
 
 
-def read_traffic(kernel_name):
-    """HBM bytes per launch of `kernel_name` from the committed rocprofv3 PMC
-    summary (profiles/hbm_traffic.md), or None if it was not measured."""
+def read_traffic(workload):
+    """HBM bytes per launch for `workload` ("headline" or a key of `also`)
+    from the committed rocprofv3 PMC summary (profiles/hbm_traffic.md: two
+    runs, FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading
+    for a plain 1 GiB copy), or None if it was not measured."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 2 and cells[0] == kernel_name:
+        if len(cells) >= 2 and cells[0] == workload:
             try:
                 return int(cells[-1])
             except ValueError:
@@ -212,7 +214,7 @@ def main():
     ms = time_launches(step, args.steps, args.warmup)
     flops = 2.0 * m * n * k
     value = flops / (ms * 1e-3) / 1e12
-    traffic = read_traffic(kernel)
+    traffic = read_traffic("headline")
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -259,6 +261,8 @@ def main():
         also["fp32_tall_skinny_cfg4"] = ts
         also["fp32_512_cfg1"] = run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
                                            steps * 5, 5)
+        for key, entry in also.items():
+            entry["traffic"] = read_traffic(key)
         result["also"] = also
     print(json.dumps(result), flush=True)
     del np
