@@ -175,6 +175,13 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     int group_m;
     bool c_vec;  // C rows allow 16-byte vector access (ldc, base and batch stride aligned)
+    // Split-K of the tail: tiles [0, num_full) run whole; each tile in
+    // [num_full, tiles_m*tiles_n) is cut into `split` k-ranges whose fp
+    // partials go to ws (BM*BN elements per part), and splitk_reduce_kernel
+    // sums them in part order and writes C.  split == 1: no split.
+    int num_full;
+    int split;
+    T* ws;
 };
 
 // ---------------------------------------------------------------------------
@@ -363,10 +370,16 @@ gemm_mfma_kernel(GemmArgs<T> p)
     const int wn0 = (wave % WAVES_N) * WTN;
 
     // ---- tile index: XCD-aware remap, then GROUP_M-tall column walk ----
-    const int ntiles = p.tiles_m * p.tiles_n;
+    // Blocks [0, num_full) own whole tiles; the rest are (tile, k-part) units.
     int id = blockIdx.x;
-    if ((ntiles & 7) == 0) {
-        const int per_xcd = ntiles >> 3;
+    int part = 0;
+    const bool is_split = id >= p.num_full;
+    if (is_split) {
+        const int u = id - p.num_full;
+        id = p.num_full + u / p.split;
+        part = u - (u / p.split) * p.split;
+    } else if ((p.num_full & 7) == 0) {
+        const int per_xcd = p.num_full >> 3;
         id = (id & 7) * per_xcd + (id >> 3);
     }
     const int group_span = p.group_m * p.tiles_n;
@@ -407,7 +420,10 @@ gemm_mfma_kernel(GemmArgs<T> p)
 #pragma unroll
             for (int r = 0; r < MF::NACC; ++r) acc[i][j][r] = 0;
 
-    const int nk = (p.K + BK - 1) / BK;
+    // k tiles [kt0, nk) of this block (a k-part for split units)
+    const int nk_all = (p.K + BK - 1) / BK;
+    const int kt0 = is_split ? (int)((int64_t)part * nk_all / p.split) : 0;
+    const int nk = is_split ? (int)((int64_t)(part + 1) * nk_all / p.split) : nk_all;
 
     // global tile kt -> staging set S
     auto issue = [&](auto S, int kt) {
@@ -507,66 +523,125 @@ gemm_mfma_kernel(GemmArgs<T> p)
         }
     };
 
-    // prologue: tile 0 -> LDS buffer 0 (and tile 1 -> staging set 0 if PF == 2)
+    // prologue: tile kt0 -> LDS buffer 0 (and tile kt0+1 -> staging set 0 if PF == 2)
     if (PF == 1) {
-        issue(Int<0>{}, 0);
+        issue(Int<0>{}, kt0);
         commit(Int<0>{}, 0);
     } else {
-        issue(Int<PF - 1>{}, 0);
+        issue(Int<PF - 1>{}, kt0);
         commit(Int<PF - 1>{}, 0);
-        if (nk > 1) issue(Int<0>{}, 1);
+        if (kt0 + 1 < nk) issue(Int<0>{}, kt0 + 1);
     }
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
 
     if (PF == 1) {
-        for (int kt = 0; kt < nk; ++kt) step(Int<0>{}, kt, kt & 1);
+        for (int kt = kt0; kt < nk; ++kt) step(Int<0>{}, kt, (kt - kt0) & 1);
     } else {
-        for (int kt = 0; kt < nk; kt += 2) {
+        for (int kt = kt0; kt < nk; kt += 2) {
             step(Int<0>{}, kt, 0);
             if (kt + 1 < nk) step(Int<1>{}, kt + 1, 1);
         }
     }
 
-    // ---- epilogue: C = alpha*acc + beta*C (C is not read when beta == 0) ----
+    // ---- epilogue ----
+    // Whole tile: C = alpha*acc + beta*C (C is not read when beta == 0).
+    // Split unit: the raw fp partial goes to its BM x BN slot of the
+    // workspace (row-major, tile-local); splitk_reduce_kernel finishes C.
     // With B n-contiguous, a lane owns UB consecutive columns of each row and
-    // writes them with one vector store when C allows it.
+    // writes them with one vector store when the destination allows it.
     constexpr int UB = FragB::U;
     const int q = lane / MB, jl = lane % MB;
-    const bool read_c = p.beta != (T)0;
+    T* dst;
+    int64_t ldd;
+    int row_lim, col_lim;
+    T alpha, beta;
+    bool vec_ok;
+    if (is_split) {
+        dst = p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN);
+        ldd = BN;
+        row_lim = BM;
+        col_lim = BN;
+        alpha = (T)1;
+        beta = (T)0;
+        vec_ok = true;
+    } else {
+        dst = C + (int64_t)m0 * p.ldc + n0;
+        ldd = p.ldc;
+        row_lim = p.M - m0;
+        col_lim = p.N - n0;
+        alpha = p.alpha;
+        beta = p.beta;
+        vec_ok = p.c_vec;
+    }
+    const bool read_c = beta != (T)0;
 #pragma unroll
     for (int i = 0; i < NBM; ++i)
 #pragma unroll
         for (int s = 0; s < NBN / UB; ++s) {
-            const int nb = n0 + wn0 + FragB::map(s * UB, jl);
-            const bool vec = UB > 1 && p.c_vec && nb + UB <= p.N;
+            const int nb = wn0 + FragB::map(s * UB, jl);
+            const bool vec = UB > 1 && vec_ok && nb + UB <= col_lim;
 #pragma unroll
             for (int r = 0; r < MF::NACC; ++r) {
-                const int m = m0 + wm0 + FragA::map(i, MF::row(r, q));
-                if (m >= p.M) continue;
-                T* cp = C + (int64_t)m * p.ldc + nb;
+                const int m = wm0 + FragA::map(i, MF::row(r, q));
+                if (m >= row_lim) continue;
+                T* cp = dst + (int64_t)m * ldd + nb;
                 T v[UB];
 #pragma unroll
-                for (int u = 0; u < UB; ++u) v[u] = p.alpha * acc[i][s * UB + u][r];
+                for (int u = 0; u < UB; ++u) v[u] = alpha * acc[i][s * UB + u][r];
                 if (vec) {
                     if (read_c) {
                         T c[UB];
                         CVec<T, UB>::load(cp, c);
 #pragma unroll
-                        for (int u = 0; u < UB; ++u) v[u] += p.beta * c[u];
+                        for (int u = 0; u < UB; ++u) v[u] += beta * c[u];
                     }
                     CVec<T, UB>::store(cp, v);
                 } else {
 #pragma unroll
                     for (int u = 0; u < UB; ++u)
-                        if (nb + u < p.N) {
+                        if (nb + u < col_lim) {
                             T w = v[u];
-                            if (read_c) w += p.beta * cp[u];
+                            if (read_c) w += beta * cp[u];
                             cp[u] = w;
                         }
                 }
             }
         }
+}
+
+// Split-K finish: for tail tile `slot` (tile id num_full + slot), sum the
+// `split` partials in part order (deterministic), then C = alpha*sum + beta*C.
+// One workgroup of 256 lanes per (slot, 1024-element chunk of the tile).
+template <typename T, int BM, int BN>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
+{
+    constexpr int CHUNKS = BM * BN / 1024;
+    const int slot = blockIdx.x / CHUNKS;
+    const int chunk = blockIdx.x - slot * CHUNKS;
+    const int id = p.num_full + slot;
+    const int group_span = p.group_m * p.tiles_n;
+    const int group = id / group_span;
+    const int first_m = group * p.group_m;
+    const int gsize = min(p.tiles_m - first_m, p.group_m);
+    const int in_group = id - group * group_span;
+    const int m0 = (first_m + in_group % gsize) * BM;
+    const int n0 = (in_group / gsize) * BN;
+    T* C = p.C + (int64_t)blockIdx.z * p.str_c;
+    const T* part0 = p.ws + (int64_t)slot * p.split * (BM * BN);
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+        const int e = chunk * 1024 + e4 * 256 + threadIdx.x;
+        const int row = e / BN, col = e - (e / BN) * BN;
+        const int m = m0 + row, n = n0 + col;
+        if (m >= p.M || n >= p.N) continue;
+        T sum = part0[e];
+        for (int q = 1; q < p.split; ++q) sum += part0[(int64_t)q * (BM * BN) + e];
+        T* cp = C + (int64_t)m * p.ldc + n;
+        T v = p.alpha * sum;
+        if (p.beta != (T)0) v += p.beta * *cp;
+        *cp = v;
+    }
 }
 
 }  // namespace sbx

@@ -13,7 +13,8 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, b
                        int batch, hipStream_t stream)
 {
     constexpr int V = 16 / (int)sizeof(T);
-    const dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)batch);
+    const int tiles = a.tiles_m * a.tiles_n;
+    const dim3 grid((unsigned)(a.num_full + (tiles - a.num_full) * a.split), 1, (unsigned)batch);
     const dim3 block(256);
     const int sel = (a_kc ? 8 : 0) | (b_kc ? 4 : 0) | (a_vec ? 2 : 0) | (b_vec ? 1 : 0);
 #define SBX_LAUNCH(AK, BKC, VA, VB) \
@@ -37,6 +38,13 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, b
     default: SBX_LAUNCH(true, true, V, V); break;
     }
 #undef SBX_LAUNCH
+    if (a.split > 1) {
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        constexpr int CHUNKS = BM * BN / 1024;
+        const dim3 rgrid((unsigned)((tiles - a.num_full) * CHUNKS), 1, (unsigned)batch);
+        splitk_reduce_kernel<T, BM, BN><<<rgrid, block, 0, stream>>>(a);
+    }
     return hipGetLastError();
 }
 

@@ -9,6 +9,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "../../include/sbx.h"
 #include "launch.hpp"
 
@@ -52,13 +56,14 @@ enum Cfg {
 struct CfgInfo {
     const char* name;
     int bm, bn, bk;
+    int per_cu;  // resident workgroups per CU (waves per SIMD of the config)
 };
 
 const CfgInfo kCfg[] = {
-    {"mfma_f32_256x256x16_w2x2", 256, 256, 16}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16},
-    {"mfma_f32_128x64x32_w2x2", 128, 64, 32},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32},
-    {"mfma_f64_128x128x16_w2x2", 128, 128, 16}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16},
-    {"mfma_f64_64x128x16_w2x2", 64, 128, 16},   {"generic_64x64x16", 64, 64, 16},
+    {"mfma_f32_256x256x16_w2x2", 256, 256, 16, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
+    {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
+    {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
+    {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"generic_64x64x16", 64, 64, 16, 4},
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -118,6 +123,93 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
     return ld >= (need > 1 ? need : 1) ? SBX_OK : SBX_INVALID_ARGUMENT;
 }
 
+// ---------------------------------------------------------------------------
+// Split-K of under-filled grids.  With S resident slots (CUs x workgroups per
+// CU), a grid of T tiles runs ceil(T/S) rounds; when the last round would be
+// less than 60 % full (or T < S), those tail tiles are cut into `split`
+// k-ranges so the last round is full, and a second kernel sums the parts in
+// fixed order (deterministic).  The partials live in a workspace cached per
+// (device, stream): calls on one stream are ordered, so they can share it; the
+// first call that needs more memory grows it (the only allocation on the GEMM
+// path, once per stream and size).
+// ---------------------------------------------------------------------------
+constexpr int kMaxSplit = 8;
+
+struct SplitPlan {
+    int num_full;
+    int split;
+    int rem;
+};
+
+SplitPlan plan_split(int64_t tiles, int64_t slots, int64_t nk, int64_t batch)
+{
+    SplitPlan none{(int)tiles, 1, 0};
+    if (batch > 1 || nk < 4) return none;
+    int64_t rem, split;
+    if (tiles >= slots) {
+        rem = tiles % slots;
+        if (rem == 0 || rem * 10 >= slots * 6) return none;
+    } else {
+        rem = tiles;
+    }
+    split = slots / rem;
+    if (split > kMaxSplit) split = kMaxSplit;
+    if (split > nk / 2) split = nk / 2;
+    if (split < 2) return none;
+    return SplitPlan{(int)(tiles - rem), (int)split, (int)rem};
+}
+
+std::mutex g_cu_mutex;
+int g_cu_count[64] = {0};
+
+int cu_count()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> g(g_cu_mutex);
+    if (!g_cu_count[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            return 256;
+        g_cu_count[dev] = cus;
+    }
+    return g_cu_count[dev];
+}
+
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+// never destroyed: freeing device memory during process teardown is unsafe
+std::map<std::pair<int, hipStream_t>, Workspace>* g_ws =
+    new std::map<std::pair<int, hipStream_t>, Workspace>();
+
+// A workspace of at least `bytes` for `stream`, or nullptr.
+void* stream_workspace(hipStream_t stream, size_t bytes)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> g(g_ws_mutex);
+    Workspace& w = (*g_ws)[{dev, stream}];
+    if (w.bytes < bytes) {
+        if (w.base) {
+            if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+            (void)hipFree(w.base);
+            w.base = nullptr;
+            w.bytes = 0;
+        }
+        size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
+        if (hipMalloc(&w.base, nb) != hipSuccess) {
+            w.base = nullptr;
+            return nullptr;
+        }
+        w.bytes = nb;
+    }
+    return w.base;
+}
+
 hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan pb,
                       const Problem& p, int nb, hipStream_t s)
 {
@@ -155,7 +247,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, OperandPlan pa, OperandPlan 
 }
 
 template <typename T>
-int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen)
+int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen,
+        SplitPlan* chosen_split)
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
@@ -165,8 +258,20 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         if (algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
         cfg = GENERIC;
     }
+    const CfgInfo& info = kCfg[cfg];
+    const int64_t tiles = cdiv(p.m, info.bm) * cdiv(p.n, info.bn);
+    SplitPlan sp{(int)tiles, 1, 0};
+    if (cfg != GENERIC && !quick)
+        sp = plan_split(tiles, (int64_t)cu_count() * info.per_cu, cdiv(p.k, info.bk), p.batch);
     if (chosen) *chosen = cfg;
+    if (chosen_split) *chosen_split = sp;
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
+    void* ws = nullptr;
+    if (sp.split > 1) {
+        ws = stream_workspace(stream, (size_t)sp.rem * sp.split * info.bm *
+                                                         info.bn * sizeof(T));
+        if (!ws) sp = SplitPlan{(int)tiles, 1, 0};  // no memory: run unsplit
+    }
 
     for (int64_t b0 = 0; b0 < p.batch; b0 += kMaxGridZ) {
         const int nb = (int)((p.batch - b0) < kMaxGridZ ? (p.batch - b0) : kMaxGridZ);
@@ -189,6 +294,9 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.group_m = a.tiles_m < 8 ? a.tiles_m : 8;
             a.c_vec = p.ldc % (16 / (int64_t)sizeof(T)) == 0 && (uintptr_t)a.C % 16 == 0 &&
                       (p.batch <= 1 || p.str_c % (16 / (int64_t)sizeof(T)) == 0);
+            a.num_full = sp.num_full;
+            a.split = sp.split;
+            a.ws = (T*)ws;
             const size_t elem = sizeof(T);
             const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
                                                 a.A, elem);
@@ -204,7 +312,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
 int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
               int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
               int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
-              void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, Cfg* chosen)
+              void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, Cfg* chosen,
+              SplitPlan* chosen_split)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
@@ -246,8 +355,10 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
 
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
-        return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen);
-    return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen);
+        return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen,
+                          chosen_split);
+    return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
+                       chosen_split);
 }
 
 }  // namespace
@@ -262,7 +373,7 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
 {
     if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
     return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
-                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, nullptr);
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, nullptr, nullptr);
 }
 
 int sbx_sgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
@@ -310,10 +421,14 @@ int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, in
     // 16-byte aligned stand-in addresses: selection never dereferences them.
     const void* fake = (const void*)(uintptr_t)0x1000;
     sbx::Cfg cfg = sbx::GENERIC;
+    sbx::SplitPlan sp{0, 1, 0};
     int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda, 0,
-                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO, &cfg);
+                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO, &cfg, &sp);
     if (st != SBX_OK) return st;
-    snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
+    if (sp.split > 1)
+        snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);
+    else
+        snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
     return SBX_OK;
 }
 
