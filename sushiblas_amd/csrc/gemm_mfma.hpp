@@ -469,14 +469,14 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // the last group overlap the fragment reads of the next tile's group 0.
     // With PF == 2, staging set S holds tile kt + 1 on entry and set S ^ 1
     // receives tile kt + 2, so the LDS writes never wait on fresh loads.
+    // The loads, LDS writes and next-tile reads are issued unconditionally so
+    // that each region is one basic block the scheduling hints can interleave:
+    // past the last k tile the buffer loads are masked (k_rem <= 0 or the
+    // next part's data) and what they write to the idle LDS buffer is unused.
     auto step = [&](auto S, int kt, int cur) {
         constexpr int st = decltype(S)::value;
-        const bool more = kt + 1 < nk;
-        if (PF == 1) {
-            if (more) issue(Int<0>{}, kt + 1);
-        } else {
-            if (kt + 2 < nk) issue(Int<st ^ 1>{}, kt + 2);
-        }
+        if (PF == 1) issue(Int<0>{}, kt + 1);
+        else issue(Int<st ^ 1>{}, kt + 2);
 #pragma unroll
         for (int g = 0; g + 1 < G; ++g) {
             if (((g + 1) & 1) == 0) read_frags(Int<0>{}, cur, g + 1);
@@ -484,7 +484,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
             if ((g & 1) == 0) mma(Int<0>{});
             else mma(Int<1>{});
         }
-        if (more) commit(Int<PF == 1 ? 0 : st>{}, cur ^ 1);
+        commit(Int<PF == 1 ? 0 : st>{}, cur ^ 1);
         // region A: loads first, then fragment reads, then the LDS writes,
         // each memory instruction followed by a slice of the MFMAs
         {
@@ -509,17 +509,17 @@ gemm_mfma_kernel(GemmArgs<T> p)
             __builtin_amdgcn_sched_group_barrier(0x008, mf, 0);
         }
         __syncthreads();
-        if (more) read_frags(Int<0>{}, cur ^ 1, 0);
+        read_frags(Int<0>{}, cur ^ 1, 0);
         mma(Int<1>{});
         // region B: the next tile's group-0 reads spread over the last group
         {
             constexpr int per = MPG / RPG > 0 ? MPG / RPG : 1;
 #pragma unroll
             for (int x = 0; x < RPG; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-                __builtin_amdgcn_sched_group_barrier(0x008, per, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, MPG, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, MPG, 0);
         }
     };
 
@@ -530,7 +530,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     } else {
         issue(Int<PF - 1>{}, kt0);
         commit(Int<PF - 1>{}, 0);
-        if (kt0 + 1 < nk) issue(Int<0>{}, kt0 + 1);
+        issue(Int<0>{}, kt0 + 1);
     }
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
