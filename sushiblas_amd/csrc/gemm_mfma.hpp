@@ -612,11 +612,14 @@ gemm_mfma_kernel(GemmArgs<T> p)
 
 // Split-K finish: for tail tile `slot` (tile id num_full + slot), sum the
 // `split` partials in part order (deterministic), then C = alpha*sum + beta*C.
-// One workgroup of 256 lanes per (slot, 1024-element chunk of the tile).
+// One lane per element, one workgroup of 256 lanes per (slot, 256-element
+// chunk); all of a lane's partial loads are issued before the sum.
+constexpr int kMaxSplitParts = 8;
+
 template <typename T, int BM, int BN>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
 {
-    constexpr int CHUNKS = BM * BN / 1024;
+    constexpr int CHUNKS = BM * BN / 256;
     const int slot = blockIdx.x / CHUNKS;
     const int chunk = blockIdx.x - slot * CHUNKS;
     const int id = p.num_full + slot;
@@ -625,23 +628,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
     const int first_m = group * p.group_m;
     const int gsize = min(p.tiles_m - first_m, p.group_m);
     const int in_group = id - group * group_span;
-    const int m0 = (first_m + in_group % gsize) * BM;
-    const int n0 = (in_group / gsize) * BN;
-    T* C = p.C + (int64_t)blockIdx.z * p.str_c;
-    const T* part0 = p.ws + (int64_t)slot * p.split * (BM * BN);
+    const int e = chunk * 256 + threadIdx.x;
+    const int m = (first_m + in_group % gsize) * BM + e / BN;
+    const int n = (in_group / gsize) * BN + e % BN;
+    if (m >= p.M || n >= p.N) return;
+    const T* part0 = p.ws + (int64_t)slot * p.split * (BM * BN) + e;
+    T v[kMaxSplitParts];
 #pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) {
-        const int e = chunk * 1024 + e4 * 256 + threadIdx.x;
-        const int row = e / BN, col = e - (e / BN) * BN;
-        const int m = m0 + row, n = n0 + col;
-        if (m >= p.M || n >= p.N) continue;
-        T sum = part0[e];
-        for (int q = 1; q < p.split; ++q) sum += part0[(int64_t)q * (BM * BN) + e];
-        T* cp = C + (int64_t)m * p.ldc + n;
-        T v = p.alpha * sum;
-        if (p.beta != (T)0) v += p.beta * *cp;
-        *cp = v;
-    }
+    for (int q = 0; q < kMaxSplitParts; ++q) v[q] = q < p.split ? part0[(int64_t)q * (BM * BN)] : (T)0;
+    T sum = v[0];
+#pragma unroll
+    for (int q = 1; q < kMaxSplitParts; ++q)
+        if (q < p.split) sum += v[q];
+    T* cp = p.C + (int64_t)blockIdx.z * p.str_c + (int64_t)m * p.ldc + n;
+    T out = p.alpha * sum;
+    if (p.beta != (T)0) out += p.beta * *cp;
+    *cp = out;
 }
 
 }  // namespace sbx

@@ -29,7 +29,7 @@ hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, 
 // (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp):
 // (T, BM, BN, BK, waves along M, waves along N, prefetch depth, waves/SIMD)
 #define SBX_MFMA_CONFIGS(X)  \
-    X(float, 256, 256, 16, 2, 2, 1, 1) \
+    X(float, 256, 256, 32, 2, 2, 1, 1) \
     X(float, 128, 128, 16, 2, 2, 2, 2) \
     X(float, 128, 64, 32, 2, 2, 2, 2) \
     X(float, 64, 128, 32, 2, 2, 2, 2) \

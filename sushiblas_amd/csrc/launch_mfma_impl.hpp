@@ -41,7 +41,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, b
     if (a.split > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        constexpr int CHUNKS = BM * BN / 1024;
+        constexpr int CHUNKS = BM * BN / 256;
         const dim3 rgrid((unsigned)((tiles - a.num_full) * CHUNKS), 1, (unsigned)batch);
         splitk_reduce_kernel<T, BM, BN><<<rgrid, block, 0, stream>>>(a);
     }

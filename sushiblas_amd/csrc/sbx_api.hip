@@ -60,7 +60,7 @@ struct CfgInfo {
 };
 
 const CfgInfo kCfg[] = {
-    {"mfma_f32_256x256x16_w2x2", 256, 256, 16, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
+    {"mfma_f32_256x256x32_w2x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"generic_64x64x16", 64, 64, 16, 4},
@@ -133,7 +133,7 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 // first call that needs more memory grows it (the only allocation on the GEMM
 // path, once per stream and size).
 // ---------------------------------------------------------------------------
-constexpr int kMaxSplit = 8;
+constexpr int kMaxSplit = kMaxSplitParts;
 
 struct SplitPlan {
     int num_full;
@@ -215,7 +215,7 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan p
 {
     switch (cfg) {
     case F32_256x256:
-        return launch_mfma<float, 256, 256, 16, 2, 2, 1, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_128x128:
         return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_128x64:

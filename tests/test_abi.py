@@ -83,7 +83,7 @@ def test_noop_cases_need_no_device():
 
 
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
-    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x16_w2x2"),
+    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w2x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2+splitk2"),
     (0, 0, 0, 0, 512, 512, 512, "mfma_f32_128x128x16_w2x2+splitk8"),
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
