@@ -14,7 +14,8 @@ Printed as one JSON line.  Besides the contract fields it carries:
   parity        -- normwise error of the GPU result vs the oracle on the
                    sampled rows (identical input bits)
   also          -- the other BASELINE configs timed the same way (fp64 8192^3,
-                   the ragged 4095x3001x2047 transposes, tall-skinny, 512^3)
+                   the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), and
+                   the fused GEMM+ReLU epilogue against GEMM followed by ReLU
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
                        [--cpu-seconds S]
@@ -171,6 +172,38 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
     return out
 
 
+def run_fused_config(m, n, k, seed, steps, warmup):
+    """GEMM+ReLU as one fused launch (sbx_gemm_fused) against the unfused pair
+    (sbx_gemm_ex, then sbx_relu over C): the caller pattern of the reference's
+    integration tests (tests/runtime/test_framework_sim.cpp:51-57)."""
+    import torch
+    import sushiblas_amd as sbx
+    A = torch.empty(m * k, dtype=torch.float32, device="cuda")
+    B = torch.empty(k * n, dtype=torch.float32, device="cuda")
+    C = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    sbx.fill_uniform(A, seed, 0)
+    sbx.fill_uniform(B, seed, 1)
+    C.zero_()
+
+    def fused():
+        sbx.gemm_fused(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0)
+
+    def unfused():
+        sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0)
+        sbx.relu(C)
+
+    ms_f = time_launches(fused, steps, warmup)
+    ms_u = time_launches(unfused, steps, warmup)
+    flops = 2.0 * m * n * k
+    out = {"kernel": sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n) + "+relu",
+           "ms": round(ms_f, 4), "tflops": round(flops / (ms_f * 1e-3) / 1e12, 3),
+           "pct_peak": round(100 * flops / (ms_f * 1e-3) / 1e12 / PEAK["f32"], 2),
+           "ms_unfused": round(ms_u, 4), "speedup_vs_unfused": round(ms_u / ms_f, 3)}
+    del A, B, C
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -261,6 +294,10 @@ def main():
         also["fp32_tall_skinny_cfg4"] = ts
         also["fp32_512_cfg1"] = run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
                                            steps * 5, 5)
+        also["fp32_gemm_relu_layer_512x1024x1024"] = run_fused_config(512, 1024, 1024, SEED + 6,
+                                                                      steps * 5, 5)
+        also["fp32_gemm_relu_8192x8192x256"] = run_fused_config(8192, 8192, 256, SEED + 7,
+                                                                steps * 2, 3)
         for key, entry in also.items():
             entry["traffic"] = read_traffic(key)
         result["also"] = also

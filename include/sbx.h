@@ -14,7 +14,9 @@
  *     memory (or pinned host memory mapped into the device address space).
  *     The library never frees or retains a caller pointer.
  *   - Launches are asynchronous on `stream` (NULL = the null stream of the
- *     current device).  Nothing is allocated on the GEMM path.
+ *     current device).  The only allocation is the split-K workspace for
+ *     under-filled grids: cached per (device, stream), grown with hipMalloc
+ *     the first time a larger one is needed, reused after that.
  *   - Return value is a status code (sbx_status); nothing throws across the
  *     ABI.  The C++ layer turns codes into std::runtime_error, as the
  *     reference's SB_THROW_IF does (include/SushiBLAS/core/logger.hpp:316-323).
@@ -87,6 +89,26 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
                 int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
                 int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
                 void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo);
+
+/* Epilogues that can be fused into the GEMM (no counterpart on the
+ * reference's GEMM path, where they are separate tasks). */
+typedef enum sbx_epilogue { SBX_EPILOGUE_NONE = 0, SBX_EPILOGUE_RELU = 1 } sbx_epilogue;
+
+/* C = epilogue(alpha*op(A)*op(B) + beta*C), same arguments as sbx_gemm_ex.
+ * SBX_EPILOGUE_RELU fuses the caller pattern of the reference's integration
+ * tests -- Level3::gemm followed by NonLinearOps::relu on C
+ * (tests/runtime/test_framework_sim.cpp:51-57,109-110; ReLU is
+ * src/ops/math/nonlinear/relu.cpp:38-41: x > 0 ? x : 0) -- into one kernel,
+ * saving the extra read and write of C. */
+int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                   int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                   int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                   void* C, int64_t ldc, int64_t str_c, int64_t batch, int epilogue);
+
+/* x[i] = x[i] > 0 ? x[i] : 0 for n contiguous elements of dtype: the
+ * stand-alone ReLU (replaces the body of NonLinearOps::relu,
+ * src/ops/math/nonlinear/relu.cpp:38-41, for FLOAT32/FLOAT64). */
+int sbx_relu(void* stream, int dtype, void* x, int64_t n);
 
 /* Name of the kernel the dispatcher would launch for this problem (tiling
  * heuristics introspection for benchmarks).  Pointers are assumed 16-byte

@@ -18,5 +18,6 @@ from .sbo import (  # noqa: F401
     philox4x32_10,
     fill_uniform,
     fill_normal,
+    relu,
     num_threads,
 )

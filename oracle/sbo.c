@@ -260,6 +260,19 @@ DEFINE_ERR(sbo_rel_fro_err_f32, float)
 DEFINE_ERR(sbo_rel_fro_err_f64, double)
 
 /* ------------------------------------------------------------------------ */
+/* ReLU (relu.cpp:38-41).                                                    */
+/* ------------------------------------------------------------------------ */
+void sbo_relu_f32(float* x, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) x[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+void sbo_relu_f64(double* x, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) x[i] = x[i] > 0.0 ? x[i] : 0.0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).                        */
 /* ------------------------------------------------------------------------ */
 void sbo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])

@@ -73,6 +73,12 @@ double sbo_rel_fro_err_f32(int64_t rows, int64_t cols, const float* X, int64_t l
 double sbo_rel_fro_err_f64(int64_t rows, int64_t cols, const double* X, int64_t ldx,
                            const double* Y, int64_t ldy);
 
+/* ReLU in place over n elements, as the reference defines it
+ * (src/ops/math/nonlinear/relu.cpp:38-41): x > 0 ? x : 0, so NaN and -0
+ * become +0. */
+void sbo_relu_f32(float* x, int64_t n);
+void sbo_relu_f64(double* x, int64_t n);
+
 /* Philox4x32-10: out[0..3] = philox(ctr[0..3], key[0..1]). */
 void sbo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 

@@ -59,6 +59,10 @@ def _load():
         f = getattr(lib, name)
         f.restype = None
         f.argtypes = [_vp, _i64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_double]
+    for name in ("sbo_relu_f32", "sbo_relu_f64"):
+        f = getattr(lib, name)
+        f.restype = None
+        f.argtypes = [_vp, _i64]
     lib.sbo_num_threads.restype = ctypes.c_int
     lib.sbo_num_threads.argtypes = []
     _lib = lib
@@ -142,6 +146,14 @@ def fill_normal(n: int, dtype, seed: int, stream: int, scale: float = 1.0) -> np
     f = lib.sbo_fill_normal_f32 if out.dtype == np.float32 else lib.sbo_fill_normal_f64
     f(_ptr(out), out.size, seed, stream, float(scale))
     return out
+
+
+def relu(x: np.ndarray) -> np.ndarray:
+    """In-place ReLU as the reference defines it: x > 0 ? x : 0."""
+    lib = _load()
+    f = lib.sbo_relu_f32 if x.dtype == np.float32 else lib.sbo_relu_f64
+    f(_ptr(x), x.size)
+    return x
 
 
 def num_threads() -> int:

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libsbx.so")
 
 F32, F64 = 0, 1
 ALGO_AUTO, ALGO_GENERIC, ALGO_MFMA = 0, 1, 2
+EPILOGUE_NONE, EPILOGUE_RELU = 0, 1
 STATUS = {0: "SBX_OK", 1: "SBX_INVALID_ARGUMENT", 2: "SBX_UNSUPPORTED", 3: "SBX_HIP_ERROR"}
 
 _lib = None
@@ -64,6 +65,11 @@ def lib() -> ctypes.CDLL:
         f.restype = i32
         f.argtypes = [vp, i32, i32, i32, i64, i64, i64, real, vp, i64, i64, vp, i64, i64, real,
                       vp, i64, i64, i64]
+    L.sbx_gemm_fused.restype = i32
+    L.sbx_gemm_fused.argtypes = [vp, i32, i32, i32, i32, i64, i64, i64, vp, vp, i64, i64, vp,
+                                 i64, i64, vp, vp, i64, i64, i64, i32]
+    L.sbx_relu.restype = i32
+    L.sbx_relu.argtypes = [vp, i32, vp, i64]
     L.sbx_gemm_select.restype = i32
     L.sbx_gemm_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64,
                                   ctypes.c_char_p, ctypes.c_size_t]
@@ -119,6 +125,27 @@ def gemm_ex(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb
                            k, ctypes.byref(a), _ptr(A), lda, str_a, _ptr(B), ldb, str_b,
                            ctypes.byref(b), _ptr(C), ldc, str_c, batch, algo)
     _check(st, "sbx_gemm_ex")
+
+
+def gemm_fused(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb, str_b,
+               beta, C, ldc, str_c, batch=1, epilogue=EPILOGUE_RELU, stream=None) -> None:
+    """sbx_gemm_fused: C = epilogue(alpha*op(A)*op(B) + beta*C) in one launch."""
+    real = ctypes.c_float if dtype == F32 else ctypes.c_double
+    a = real(alpha)
+    b = real(beta)
+    st = lib().sbx_gemm_fused(_stream(stream), dtype, int(layout), int(transA), int(transB), m,
+                              n, k, ctypes.byref(a), _ptr(A), lda, str_a, _ptr(B), ldb, str_b,
+                              ctypes.byref(b), _ptr(C), ldc, str_c, batch, int(epilogue))
+    _check(st, "sbx_gemm_fused")
+
+
+def relu(x, n=None, dtype=None, stream=None) -> None:
+    """sbx_relu in place: x = x > 0 ? x : 0 over n contiguous elements."""
+    if dtype is None:
+        dtype = F32 if x.element_size() == 4 else F64
+    if n is None:
+        n = x.numel()
+    _check(lib().sbx_relu(_stream(stream), dtype, _ptr(x), n), "sbx_relu")
 
 
 def sgemm(layout, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,

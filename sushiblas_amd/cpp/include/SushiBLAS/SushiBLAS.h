@@ -5,6 +5,7 @@
 #include <SushiBLAS/core/errors.hpp>
 #include <SushiBLAS/engine.hpp>
 #include <SushiBLAS/ops/blas.hpp>
+#include <SushiBLAS/ops/math/nonlinear.hpp>
 #include <SushiBLAS/storage.hpp>
 #include <SushiBLAS/tensor.hpp>
 #include <SushiRuntime/SushiRuntime.h>

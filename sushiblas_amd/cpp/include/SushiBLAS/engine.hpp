@@ -6,6 +6,7 @@
 #include <SushiBLAS/core/common.hpp>
 #include <SushiBLAS/core/errors.hpp>
 #include <SushiBLAS/ops/blas.hpp>
+#include <SushiBLAS/ops/math/nonlinear.hpp>
 #include <SushiBLAS/storage.hpp>
 #include <SushiBLAS/tensor.hpp>
 #include <SushiRuntime/SushiRuntime.h>
@@ -23,6 +24,8 @@ namespace SushiBLAS
 
             Core::Layout get_layout() const { return default_layout_; }
             BLASOps blas() { return BLASOps(*this); }
+            /** @brief Activations (engine.hpp:118 of the reference); relu only. */
+            NonLinearOps nonlinear() { return NonLinearOps(*this); }
 
             SushiRuntime::Execution::RuntimeContext& get_context() { return context_; }
             SushiRuntime::Graph::TaskGraph& get_graph() { return graph_; }

@@ -271,6 +271,21 @@ namespace SushiRuntime
         /** @brief Optional observer called for each task as it is issued. */
         using TraceHook = std::function<void(const TaskMetadata&)>;
 
+        /** @brief What a fuser needs to know about a task (the reference's
+         *  TaskMetadata is meant "for profilers/fusers", gemm.cpp:126; this
+         *  backend implements one fusion: a GEMM immediately followed by a ReLU
+         *  on exactly its output runs as one kernel with a ReLU epilogue). */
+        struct FusionHook
+        {
+            enum Kind { NONE, PRODUCER, RELU } kind = NONE;
+            void* base = nullptr;     // storage base pointer of the output region
+            size_t offset_bytes = 0;  // first byte of the region in that storage
+            int64_t elements = 0;     // contiguous elements in the region
+            int dtype = -1;           // element type tag
+            HostWork with_relu;       // PRODUCER: the same work with the ReLU fused
+            const char* fused_name = nullptr;  // PRODUCER: task name once fused
+        };
+
         /** @brief Record-then-execute task list (graph/task_graph.hpp:55-124). */
         class TaskGraph
         {
@@ -287,12 +302,23 @@ namespace SushiRuntime
                               const std::vector<void*>& write_access, HostWork work,
                               const std::vector<Execution::Event>& dependencies = {});
 
+                /** @brief As above, with the task's fusion description. */
+                void add_task(const TaskMetadata& meta, const std::vector<void*>& read_access,
+                              const std::vector<void*>& write_access, HostWork work,
+                              FusionHook fusion,
+                              const std::vector<Execution::Event>& dependencies = {});
+
                 /** @brief Issue every recorded task in order; returns an Event that
-                 *  completes when all of them (and the staging copies) have. */
+                 *  completes when all of them (and the staging copies) have.  A
+                 *  PRODUCER task directly followed by a RELU task over the same
+                 *  region (same base, offset, element count and type, no extra
+                 *  dependencies) is issued once, as its fused form. */
                 Execution::Event execute();
 
                 size_t pending() const;
                 void set_trace_hook(TraceHook hook);
+                /** @brief Turn GEMM+ReLU fusion on (default) or off. */
+                void set_fusion(bool enabled);
 
             private:
                 struct Task
@@ -301,11 +327,13 @@ namespace SushiRuntime
                     std::vector<void*> reads, writes;
                     HostWork work;
                     std::vector<Execution::Event> deps;
+                    FusionHook fusion;
                 };
                 Execution::RuntimeContext& ctx_;
                 mutable std::mutex mu_;
                 std::vector<Task> tasks_;
                 TraceHook trace_;
+                bool fusion_ = true;
         };
     } // namespace Graph
 } // namespace SushiRuntime

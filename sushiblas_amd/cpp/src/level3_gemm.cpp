@@ -6,6 +6,9 @@
 // write sets from the storage base pointers, the "blas.lvl3.gemm" metadata.
 // The recorded closure calls the C ABI (include/sbx.h) on the context's HIP
 // stream where the reference's gemm_dispatch<T> (gemm.cpp:44-79) calls oneMKL.
+// The task also carries a fusion description (its output run and a ReLU-fused
+// form of the same work), which TaskGraph::execute() uses when a ReLU over
+// exactly that run is recorded next.
 #include <SushiBLAS/engine.hpp>
 #include <SushiBLAS/ops/blas/level3.hpp>
 
@@ -72,38 +75,64 @@ namespace SushiBLAS
         meta.set_param(2, transA);
         meta.set_param(3, transB);
 
+        // The elements this GEMM writes: batch blocks of m*n (ldc is the
+        // shape's own extent), one contiguous run when the blocks abut.  A ReLU
+        // recorded right after it over exactly that run may be fused into it.
+        SushiRuntime::Graph::FusionHook fusion;
+        const bool one_run = batch_size == 1 || str_c == m * n;
+        if (one_run && C.storage && C.storage->data_ptr && m > 0 && n > 0)
+        {
+            fusion.kind = SushiRuntime::Graph::FusionHook::PRODUCER;
+            fusion.base = C.storage->data_ptr;
+            fusion.offset_bytes = C.offset_bytes();
+            fusion.elements = batch_size * m * n;
+            fusion.dtype = static_cast<int>(C.dtype);
+            fusion.fused_name = "blas.lvl3.gemm+relu";
+        }
+
         auto& graph = engine_.get_graph();
         switch (A.dtype)
         {
             case Core::DataType::FLOAT32:
             {
-                graph.add_task(meta, reads, writes,
-                    [=, pA = A.device_data_as<float>(), pB = B.device_data_as<float>(),
-                     pC = C.device_data_as<float>()](Queue& q, const std::vector<Event>&) -> Event
+                auto work = [=, pA = A.device_data_as<float>(), pB = B.device_data_as<float>(),
+                             pC = C.device_data_as<float>()](int epilogue)
+                {
+                    return [=](Queue& q, const std::vector<Event>&) -> Event
                     {
-                        const int st = sbx_sgemm_strided_batched(q.native(), layout, tA, tB, m, n, k,
-                                                                 alpha, pA, lda, str_a, pB, ldb, str_b,
-                                                                 beta, pC, ldc, str_c, batch_size);
+                        const int st = sbx_gemm_fused(q.native(), SBX_F32, layout, tA, tB, m, n, k,
+                                                      &alpha, pA, lda, str_a, pB, ldb, str_b, &beta,
+                                                      pC, ldc, str_c, batch_size, epilogue);
                         SB_THROW_IF(st != SBX_OK, "GEMM [{}x{}x{}, batch {}] failed: {}", m, n, k,
                                     batch_size, sbx_status_string(st));
                         return Event();
-                    });
+                    };
+                };
+                if (fusion.kind != SushiRuntime::Graph::FusionHook::NONE)
+                    fusion.with_relu = work(SBX_EPILOGUE_RELU);
+                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion));
                 break;
             }
             case Core::DataType::FLOAT64:
             {
-                graph.add_task(meta, reads, writes,
-                    [=, alpha_d = static_cast<double>(alpha), beta_d = static_cast<double>(beta),
-                     pA = A.device_data_as<double>(), pB = B.device_data_as<double>(),
-                     pC = C.device_data_as<double>()](Queue& q, const std::vector<Event>&) -> Event
+                auto work = [=, alpha_d = static_cast<double>(alpha),
+                             beta_d = static_cast<double>(beta), pA = A.device_data_as<double>(),
+                             pB = B.device_data_as<double>(),
+                             pC = C.device_data_as<double>()](int epilogue)
+                {
+                    return [=](Queue& q, const std::vector<Event>&) -> Event
                     {
-                        const int st = sbx_dgemm_strided_batched(q.native(), layout, tA, tB, m, n, k,
-                                                                 alpha_d, pA, lda, str_a, pB, ldb, str_b,
-                                                                 beta_d, pC, ldc, str_c, batch_size);
+                        const int st = sbx_gemm_fused(q.native(), SBX_F64, layout, tA, tB, m, n, k,
+                                                      &alpha_d, pA, lda, str_a, pB, ldb, str_b,
+                                                      &beta_d, pC, ldc, str_c, batch_size, epilogue);
                         SB_THROW_IF(st != SBX_OK, "GEMM [{}x{}x{}, batch {}] failed: {}", m, n, k,
                                     batch_size, sbx_status_string(st));
                         return Event();
-                    });
+                    };
+                };
+                if (fusion.kind != SushiRuntime::Graph::FusionHook::NONE)
+                    fusion.with_relu = work(SBX_EPILOGUE_RELU);
+                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion));
                 break;
             }
             case Core::DataType::HALF:

@@ -4,6 +4,7 @@
 #include <SushiRuntime/SushiRuntime.h>
 
 #include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <unordered_set>
@@ -248,8 +249,23 @@ namespace SushiRuntime
                                  const std::vector<void*>& write_access, HostWork work,
                                  const std::vector<Execution::Event>& dependencies)
         {
+            add_task(meta, read_access, write_access, std::move(work), FusionHook{}, dependencies);
+        }
+
+        void TaskGraph::add_task(const TaskMetadata& meta, const std::vector<void*>& read_access,
+                                 const std::vector<void*>& write_access, HostWork work,
+                                 FusionHook fusion,
+                                 const std::vector<Execution::Event>& dependencies)
+        {
             std::lock_guard<std::mutex> g(mu_);
-            tasks_.push_back(Task{meta, read_access, write_access, std::move(work), dependencies});
+            tasks_.push_back(Task{meta, read_access, write_access, std::move(work), dependencies,
+                                  std::move(fusion)});
+        }
+
+        void TaskGraph::set_fusion(bool enabled)
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            fusion_ = enabled;
         }
 
         size_t TaskGraph::pending() const
@@ -264,14 +280,53 @@ namespace SushiRuntime
             trace_ = std::move(hook);
         }
 
+        namespace
+        {
+            // A producer and the ReLU right after it cover the same elements:
+            // running the producer's fused form instead of the pair writes the
+            // same values and saves the ReLU's read and write of the region.
+            bool fusable(const FusionHook& producer, const FusionHook& relu,
+                         const std::vector<Execution::Event>& relu_deps)
+            {
+                return producer.kind == FusionHook::PRODUCER && relu.kind == FusionHook::RELU &&
+                       producer.with_relu && producer.base && producer.base == relu.base &&
+                       producer.offset_bytes == relu.offset_bytes &&
+                       producer.elements == relu.elements && producer.elements > 0 &&
+                       producer.dtype == relu.dtype && relu_deps.empty();
+            }
+        } // namespace
+
         Execution::Event TaskGraph::execute()
         {
-            std::vector<Task> tasks;
+            std::vector<Task> recorded, tasks;
             TraceHook trace;
+            bool fuse = true;
             {
                 std::lock_guard<std::mutex> g(mu_);
-                tasks.swap(tasks_);
+                recorded.swap(tasks_);
                 trace = trace_;
+                fuse = fusion_;
+            }
+            tasks.reserve(recorded.size());
+            for (size_t i = 0; i < recorded.size(); ++i)
+            {
+                if (fuse && i + 1 < recorded.size() &&
+                    fusable(recorded[i].fusion, recorded[i + 1].fusion, recorded[i + 1].deps))
+                {
+                    Task t = std::move(recorded[i]);
+                    t.work = std::move(t.fusion.with_relu);
+                    if (t.fusion.fused_name)
+                    {
+                        t.meta.name = t.fusion.fused_name;
+                        t.meta.op_id = OpID(OpID::hash_str(t.fusion.fused_name,
+                                                           std::strlen(t.fusion.fused_name)));
+                    }
+                    t.fusion = FusionHook{};
+                    tasks.push_back(std::move(t));
+                    ++i;
+                    continue;
+                }
+                tasks.push_back(std::move(recorded[i]));
             }
             Execution::Queue& q = ctx_.get_queue();
             if (tasks.empty()) return q.record();

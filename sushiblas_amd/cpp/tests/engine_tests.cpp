@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <limits>
 #include <memory>
 #include <sstream>
 #include <string>
@@ -377,10 +378,21 @@ TEST_CASE(FrameworkSimDeepForwardPass, true)  // test_framework_sim.cpp:10-73
         weights.push_back(W);
         activations.push_back(engine.create_tensor({batch_size, features}));
     }
-    // ReLU between layers is the identity on these positive values
-    for (int i = 0; i < num_layers; ++i) engine.blas().gemm(activations[i], weights[i], activations[i + 1]);
+    std::vector<std::string> names;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
+    // as the reference records it: a ReLU after every layer but the last
+    // (the identity on these positive values)
+    for (int i = 0; i < num_layers; ++i)
+    {
+        engine.blas().gemm(activations[i], weights[i], activations[i + 1]);
+        if (i < num_layers - 1) engine.nonlinear().relu(activations[i + 1]);
+    }
     engine.execute().wait();
     CHECK(activations.back().shape[0] == batch_size && activations.back().shape[1] == features);
+    // each GEMM+ReLU pair ran as one fused task
+    CHECK(names.size() == size_t(num_layers));
+    for (int i = 0; i < num_layers - 1; ++i) CHECK(names[i] == "blas.lvl3.gemm+relu");
+    CHECK(names.back() == "blas.lvl3.gemm");
     for (int l = 1; l <= num_layers; ++l)
     {
         const double expect = std::pow(1024.0 * double(0.01f), l);
@@ -405,7 +417,11 @@ TEST_CASE(FrameworkSimParallelBatchedInference, true)  // test_framework_sim.cpp
         weights.push_back(W);
         outputs.push_back(engine.create_tensor({m, n}));
     }
-    for (int i = 0; i < num_models; ++i) engine.blas().gemm(inputs[i], weights[i], outputs[i]);
+    for (int i = 0; i < num_models; ++i)
+    {
+        engine.blas().gemm(inputs[i], weights[i], outputs[i]);
+        engine.nonlinear().relu(outputs[i]);
+    }
     engine.execute().wait();
     for (int i = 0; i < num_models; ++i)
     {
@@ -473,6 +489,191 @@ TEST_CASE(TraceHookSeesGemmMetadata, true)
     engine.execute().wait();
     CHECK(names.size() == 1 && names[0] == "blas.lvl3.gemm" && alpha_seen == 0.5f);
     verify_tensor(C, std::vector<float>(16, 2.0f), 0.0);
+}
+
+TEST_CASE(ReluRejectsUnsupportedTypes, false)
+{
+    sr::Execution::RuntimeContext local;
+    sb::Engine e(local);
+    sb::Tensor h(nullptr, {4, 4}), z(nullptr, {4, 4}), f(nullptr, {4, 4});
+    h.dtype = DataType::HALF;
+    z.dtype = DataType::COMPLEX64;
+    CHECK_THROWS(e.nonlinear().relu(h));
+    CHECK_THROWS(e.nonlinear().relu(z));
+    CHECK_THROWS(e.nonlinear().relu(f));  // no storage
+    CHECK(e.get_graph().pending() == 0);
+}
+
+namespace
+{
+    template <typename T>
+    void relu_special_values(DataType dt)
+    {
+        // relu.cpp:38-41: x > 0 ? x : 0, so NaN and -0 become +0
+        sb::Engine engine(ctx());
+        const T inf = std::numeric_limits<T>::infinity(), nan = std::numeric_limits<T>::quiet_NaN();
+        const T tiny = std::numeric_limits<T>::denorm_min();
+        std::vector<T> in = {T(-1.5), T(0), T(-0.0), T(2.25), nan, -nan, inf, -inf, tiny, -tiny, T(1e30), T(-1e30)};
+        std::vector<T> want = {0, 0, 0, T(2.25), 0, 0, inf, 0, tiny, 0, T(1e30), 0};
+        // a length that is not a multiple of the kernel's vector width
+        const int n = 1000 * int(in.size()) + 5;
+        auto t = engine.create_tensor({n}, dt);
+        std::vector<T> data(n), expect(n);
+        for (int i = 0; i < n; ++i)
+        {
+            data[i] = in[i % in.size()] * (i < int(in.size()) ? T(1) : T(1 + (i % 3)));
+            expect[i] = data[i] > T(0) ? data[i] : T(0);
+        }
+        for (size_t i = 0; i < in.size(); ++i) CHECK(std::memcmp(&expect[i], &want[i], sizeof(T)) == 0 || expect[i] == want[i]);
+        fill_tensor<T>(t, data);
+        engine.nonlinear().relu(t);
+        engine.execute().wait();
+        const T* got = t.data_as<T>();
+        for (int i = 0; i < n; ++i) CHECK(std::memcmp(&got[i], &expect[i], sizeof(T)) == 0);
+    }
+} // namespace
+
+TEST_CASE(ReluSpecialValuesFp32AndFp64, true)
+{
+    relu_special_values<float>(DataType::FLOAT32);
+    relu_special_values<double>(DataType::FLOAT64);
+}
+
+TEST_CASE(ReluOnRowSliceTouchesOnlyTheSlice, true)
+{
+    sb::Engine engine(ctx());
+    auto X = engine.create_tensor({4, 8});
+    std::vector<float> x(32);
+    for (int i = 0; i < 32; ++i) x[i] = (i % 2) ? -1.0f * i : 1.0f * i;
+    fill_tensor(X, x);
+    auto rows = X.slice(0, 1, 3);  // rows 1 and 2
+    engine.nonlinear().relu(rows);
+    engine.execute().wait();
+    const float* p = X.data_as<float>();
+    for (int i = 0; i < 32; ++i)
+    {
+        const bool inside = i >= 8 && i < 24;
+        CHECK(p[i] == (inside ? (x[i] > 0 ? x[i] : 0.0f) : x[i]));
+    }
+}
+
+namespace
+{
+    // C = relu(alpha*A*B + beta*C) through the engine, fused or not.
+    template <typename T>
+    std::vector<T> gemm_relu_via_engine(DataType dt, bool fuse, int batch, std::vector<std::string>& names)
+    {
+        sb::Engine engine(ctx());
+        engine.get_graph().set_fusion(fuse);
+        engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
+        const int m = 130, n = 97, k = 75;
+        auto A = batch > 1 ? engine.create_tensor({batch, m, k}, dt) : engine.create_tensor({m, k}, dt);
+        auto B = batch > 1 ? engine.create_tensor({batch, k, n}, dt) : engine.create_tensor({k, n}, dt);
+        auto C = batch > 1 ? engine.create_tensor({batch, m, n}, dt) : engine.create_tensor({m, n}, dt);
+        std::vector<T> a(A.num_elements), b(B.num_elements), c(C.num_elements);
+        for (size_t i = 0; i < a.size(); ++i) a[i] = T(std::sin(0.7 * i));
+        for (size_t i = 0; i < b.size(); ++i) b[i] = T(std::cos(0.3 * i));
+        for (size_t i = 0; i < c.size(); ++i) c[i] = T(0.5 * ((i % 11) - 5));
+        fill_tensor<T>(A, a);
+        fill_tensor<T>(B, b);
+        fill_tensor<T>(C, c);
+        engine.blas().gemm(A, B, C, false, false, 0.75f, 0.5f);
+        engine.nonlinear().relu(C);
+        engine.execute().wait();
+        const T* p = C.data_as<T>();
+        std::vector<T> out(p, p + C.num_elements);
+        // against a double host loop
+        double num = 0, den = 0;
+        for (int q = 0; q < batch; ++q)
+            for (int i = 0; i < m; ++i)
+                for (int j = 0; j < n; ++j)
+                {
+                    double s = 0;
+                    for (int l = 0; l < k; ++l) s += double(a[(q * m + i) * k + l]) * double(b[(q * k + l) * n + j]);
+                    double want = 0.75 * s + 0.5 * double(c[(q * m + i) * n + j]);
+                    want = want > 0 ? want : 0;
+                    const double g = out[(q * m + i) * n + j];
+                    CHECK(g >= 0);
+                    num += (g - want) * (g - want);
+                    den += want * want;
+                }
+        CHECK(std::sqrt(num / den) <= (sizeof(T) == 4 ? 1e-5 : 1e-12));
+        return out;
+    }
+} // namespace
+
+TEST_CASE(GemmReluFusedEqualsUnfused, true)
+{
+    for (int batch : {1, 3})
+    {
+        std::vector<std::string> fused_names, plain_names;
+        auto f32a = gemm_relu_via_engine<float>(DataType::FLOAT32, true, batch, fused_names);
+        auto f32b = gemm_relu_via_engine<float>(DataType::FLOAT32, false, batch, plain_names);
+        CHECK(fused_names.size() == 1 && fused_names[0] == "blas.lvl3.gemm+relu");
+        CHECK(plain_names.size() == 2 && plain_names[0] == "blas.lvl3.gemm" &&
+              plain_names[1] == "math.nonlinear.relu");
+        // same GEMM kernel, same values: the fused epilogue is bit-identical
+        CHECK(std::memcmp(f32a.data(), f32b.data(), f32a.size() * sizeof(float)) == 0);
+        fused_names.clear();
+        plain_names.clear();
+        auto f64a = gemm_relu_via_engine<double>(DataType::FLOAT64, true, batch, fused_names);
+        auto f64b = gemm_relu_via_engine<double>(DataType::FLOAT64, false, batch, plain_names);
+        CHECK(fused_names.size() == 1 && plain_names.size() == 2);
+        CHECK(std::memcmp(f64a.data(), f64b.data(), f64a.size() * sizeof(double)) == 0);
+    }
+}
+
+TEST_CASE(ReluNotFusedUnlessSameRegion, true)
+{
+    sb::Engine engine(ctx());
+    std::vector<std::string> names;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
+    auto A = engine.create_tensor({8, 8});
+    auto B = engine.create_tensor({8, 8});
+    auto C = engine.create_tensor({8, 8});
+    auto D = engine.create_tensor({8, 8});
+    std::vector<float> a(64), b(64, 1.0f), d(64);
+    for (int i = 0; i < 64; ++i) a[i] = ((i / 8) % 2) ? -1.0f : 1.0f;   // C rows alternate +-8
+    for (int i = 0; i < 64; ++i) d[i] = (i % 3) ? -2.0f : 3.0f;
+    fill_tensor(A, a);
+    fill_tensor(B, b);
+    fill_tensor(D, d);
+    // 1. ReLU on another tensor right after the GEMM: not fused
+    engine.blas().gemm(A, B, C);
+    engine.nonlinear().relu(D);
+    // 2. ReLU on part of the GEMM output: not fused
+    auto C2 = engine.create_tensor({8, 8});
+    engine.blas().gemm(A, B, C2);
+    auto top = C2.slice(0, 0, 4);
+    engine.nonlinear().relu(top);
+    // 3. GEMM into a row slice, ReLU over exactly that slice: fused
+    auto C3 = engine.create_tensor({8, 8});
+    fill_tensor(C3, std::vector<float>(64, -5.0f));
+    auto mid = C3.slice(0, 2, 6);
+    auto A4 = engine.create_tensor({4, 8});
+    fill_tensor(A4, std::vector<float>(a.begin(), a.begin() + 32));
+    engine.blas().gemm(A4, B, mid);
+    engine.nonlinear().relu(mid);
+    engine.execute().wait();
+    CHECK(names.size() == 5);
+    CHECK(names[0] == "blas.lvl3.gemm" && names[1] == "math.nonlinear.relu");
+    CHECK(names[2] == "blas.lvl3.gemm" && names[3] == "math.nonlinear.relu");
+    CHECK(names[4] == "blas.lvl3.gemm+relu");
+    // values: C untouched by ReLU, D rectified, C2 top half rectified,
+    // C3 rows 2..5 rectified GEMM rows, the rest still -5
+    const float* c = C.data_as<float>();
+    const float* dd = D.data_as<float>();
+    const float* c2 = C2.data_as<float>();
+    const float* c3 = C3.data_as<float>();
+    for (int i = 0; i < 64; ++i)
+    {
+        const float row = (i / 8 % 2) ? -8.0f : 8.0f;
+        CHECK(c[i] == row);
+        CHECK(dd[i] == (d[i] > 0 ? d[i] : 0.0f));
+        CHECK(c2[i] == (i < 32 ? (row > 0 ? row : 0.0f) : row));
+        const int r = i / 8;
+        CHECK(c3[i] == ((r >= 2 && r < 6) ? ((r % 2) ? 0.0f : 8.0f) : -5.0f));
+    }
 }
 
 TEST_CASE(LargeFp32MatchesHostLoop, true)

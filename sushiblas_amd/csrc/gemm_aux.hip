@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs<T> p)
                 T* cp = C + m * p.ldc + n;
                 T v = p.alpha * acc[i][j];
                 if (read_c) v += p.beta * *cp;
-                *cp = v;
+                *cp = p.relu ? relu_of(v) : v;
             }
         }
 }
@@ -107,11 +107,11 @@ template hipError_t launch_generic<double>(const GemmArgs<double>&, bool, bool, 
                                            hipStream_t);
 
 // ---------------------------------------------------------------------------
-// C <- beta*C over an m x n row-major window.
+// C <- beta*C over an m x n row-major window (then the ReLU when fused).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t str_c, int64_t m,
-                                                    int64_t n, T beta)
+                                                    int64_t n, T beta, int relu)
 {
     T* c = C + (int64_t)blockIdx.z * str_c;
     const int64_t total = m * n;
@@ -119,26 +119,64 @@ __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t s
          e += (int64_t)gridDim.x * 256) {
         const int64_t i = e / n, j = e - i * n;
         T* cp = c + i * ldc + j;
-        *cp = beta == (T)0 ? (T)0 : beta * *cp;
+        const T v = beta == (T)0 ? (T)0 : beta * *cp;
+        *cp = relu ? relu_of(v) : v;
     }
 }
 
 template <typename T>
 hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
-                        int batch, hipStream_t stream)
+                        int relu, int batch, hipStream_t stream)
 {
     int64_t blocks = (m * n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     if (blocks < 1) blocks = 1;
     scale_kernel<T><<<dim3((unsigned)blocks, 1, (unsigned)batch), dim3(256), 0, stream>>>(
-        C, ldc, str_c, m, n, beta);
+        C, ldc, str_c, m, n, beta, relu);
     return hipGetLastError();
 }
 
 template hipError_t launch_scale<float>(float*, int64_t, int64_t, int64_t, int64_t, float, int,
-                                        hipStream_t);
+                                        int, hipStream_t);
 template hipError_t launch_scale<double>(double*, int64_t, int64_t, int64_t, int64_t, double,
-                                         int, hipStream_t);
+                                         int, int, hipStream_t);
+
+// ---------------------------------------------------------------------------
+// Elementwise ReLU over n contiguous elements (the stand-alone form of the
+// reference's NonLinearOps::relu, src/ops/math/nonlinear/relu.cpp:38-41).
+// HBM bound: 2 * n * sizeof(T) bytes.  16-byte accesses when aligned.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) relu_kernel(T* x, int64_t n)
+{
+    constexpr int V = 16 / (int)sizeof(T);
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    const int64_t nv = ((uintptr_t)x % 16 == 0) ? n / V : 0;
+    vec_t* xv = reinterpret_cast<vec_t*>(x);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+         i += (int64_t)gridDim.x * 256) {
+        vec_t v = xv[i];
+#pragma unroll
+        for (int u = 0; u < V; ++u) v[u] = relu_of(v[u]);
+        xv[i] = v;
+    }
+    for (int64_t i = nv * V + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256)
+        x[i] = relu_of(x[i]);
+}
+
+template <typename T>
+hipError_t launch_relu(T* x, int64_t n, hipStream_t stream)
+{
+    int64_t blocks = (n / (16 / (int64_t)sizeof(T)) + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    relu_kernel<T><<<(unsigned)blocks, 256, 0, stream>>>(x, n);
+    return hipGetLastError();
+}
+
+template hipError_t launch_relu<float>(float*, int64_t, hipStream_t);
+template hipError_t launch_relu<double>(double*, int64_t, hipStream_t);
 
 }  // namespace sbx
 

@@ -182,7 +182,15 @@ struct GemmArgs {
     int num_full;
     int split;
     T* ws;
+    int relu;  // 1: C = max(alpha*A*B + beta*C, 0) with NaN -> 0 (fused ReLU epilogue)
 };
+
+// The reference's ReLU: x > 0 ? x : 0 (NaN and -0 become +0).
+template <typename T>
+__device__ inline T relu_of(T x)
+{
+    return x > (T)0 ? x : (T)0;
+}
 
 // ---------------------------------------------------------------------------
 // One operand's global -> LDS pipeline.
@@ -557,6 +565,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     int row_lim, col_lim;
     T alpha, beta;
     bool vec_ok;
+    bool relu = false;
     if (is_split) {
         dst = p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN);
         ldd = BN;
@@ -573,6 +582,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
         alpha = p.alpha;
         beta = p.beta;
         vec_ok = p.c_vec;
+        relu = p.relu != 0;
     }
     const bool read_c = beta != (T)0;
 #pragma unroll
@@ -596,6 +606,10 @@ gemm_mfma_kernel(GemmArgs<T> p)
 #pragma unroll
                         for (int u = 0; u < UB; ++u) v[u] += beta * c[u];
                     }
+                    if (relu) {
+#pragma unroll
+                        for (int u = 0; u < UB; ++u) v[u] = relu_of(v[u]);
+                    }
                     CVec<T, UB>::store(cp, v);
                 } else {
 #pragma unroll
@@ -603,7 +617,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
                         if (nb + u < col_lim) {
                             T w = v[u];
                             if (read_c) w += beta * cp[u];
-                            cp[u] = w;
+                            cp[u] = relu ? relu_of(w) : w;
                         }
                 }
             }
@@ -611,7 +625,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
 }
 
 // Split-K finish: for tail tile `slot` (tile id num_full + slot), sum the
-// `split` partials in part order (deterministic), then C = alpha*sum + beta*C.
+// `split` partials in part order (deterministic), then C = alpha*sum + beta*C
+// (and the ReLU when fused).
 // One lane per element, one workgroup of 256 lanes per (slot, 256-element
 // chunk); all of a lane's partial loads are issued before the sum.
 constexpr int kMaxSplitParts = 8;
@@ -643,7 +658,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
     T* cp = p.C + (int64_t)blockIdx.z * p.str_c + (int64_t)m * p.ldc + n;
     T out = p.alpha * sum;
     if (p.beta != (T)0) out += p.beta * *cp;
-    *cp = out;
+    *cp = p.relu ? relu_of(out) : out;
 }
 
 }  // namespace sbx

@@ -20,10 +20,14 @@ template <typename T>
 hipError_t launch_generic(const GemmArgs<T>& a, bool trans_a, bool trans_b, int batch,
                           hipStream_t stream);
 
-// C <- beta*C (beta == 0 stores zeros without reading C).
+// C <- beta*C (beta == 0 stores zeros without reading C), then ReLU if relu.
 template <typename T>
 hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
-                        int batch, hipStream_t stream);
+                        int relu, int batch, hipStream_t stream);
+
+// x <- max(x, 0) elementwise (NaN -> 0) over n contiguous elements.
+template <typename T>
+hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 
 // Tile configurations compiled into the library, one translation unit each
 // (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp):

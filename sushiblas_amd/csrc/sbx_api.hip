@@ -39,6 +39,7 @@ struct Problem {
     void* C;
     int64_t ldc, str_c;
     int64_t batch;
+    int relu;  // fused ReLU epilogue
 };
 
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
@@ -277,8 +278,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         const int nb = (int)((p.batch - b0) < kMaxGridZ ? (p.batch - b0) : kMaxGridZ);
         hipError_t e;
         if (quick) {
-            e = launch_scale<T>((T*)p.C + b0 * p.str_c, p.ldc, p.str_c, p.m, p.n, beta, nb,
-                                stream);
+            e = launch_scale<T>((T*)p.C + b0 * p.str_c, p.ldc, p.str_c, p.m, p.n, beta, p.relu,
+                                nb, stream);
         } else {
             GemmArgs<T> a;
             a.A = (const T*)p.A + b0 * p.str_a;
@@ -297,6 +298,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.num_full = sp.num_full;
             a.split = sp.split;
             a.ws = (T*)ws;
+            a.relu = p.relu;
             const size_t elem = sizeof(T);
             const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
                                                 a.A, elem);
@@ -312,10 +314,11 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
 int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
               int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
               int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
-              void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, Cfg* chosen,
-              SplitPlan* chosen_split)
+              void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, int epilogue,
+              Cfg* chosen, SplitPlan* chosen_split)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
     if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
     if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return SBX_INVALID_ARGUMENT;
     if (algo < SBX_ALGO_AUTO || algo > SBX_ALGO_MFMA) return SBX_INVALID_ARGUMENT;
@@ -351,6 +354,7 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
         p.B = A; p.ldb = lda; p.str_b = str_a;
     }
     p.k = k; p.C = C; p.ldc = ldc; p.str_c = batch > 1 ? str_c : 0; p.batch = batch;
+    p.relu = epilogue == SBX_EPILOGUE_RELU;
     if (batch <= 1) { p.str_a = 0; p.str_b = 0; }
 
     hipStream_t s = (hipStream_t)stream;
@@ -373,7 +377,31 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
 {
     if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
     return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
-                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, nullptr, nullptr);
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, SBX_EPILOGUE_NONE,
+                          nullptr, nullptr);
+}
+
+int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                   int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                   int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                   void* C, int64_t ldc, int64_t str_c, int64_t batch, int epilogue)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, SBX_ALGO_AUTO, epilogue,
+                          nullptr, nullptr);
+}
+
+int sbx_relu(void* stream, int dtype, void* x, int64_t n)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (n < 0 || (n > 0 && !x)) return SBX_INVALID_ARGUMENT;
+    if ((uintptr_t)x % (dtype == SBX_F32 ? 4 : 8)) return SBX_INVALID_ARGUMENT;
+    if (n == 0) return SBX_OK;
+    const hipError_t e = dtype == SBX_F32
+        ? sbx::launch_relu<float>((float*)x, n, (hipStream_t)stream)
+        : sbx::launch_relu<double>((double*)x, n, (hipStream_t)stream);
+    return e == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
 }
 
 int sbx_sgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,
@@ -423,7 +451,8 @@ int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, in
     sbx::Cfg cfg = sbx::GENERIC;
     sbx::SplitPlan sp{0, 1, 0};
     int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda, 0,
-                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO, &cfg, &sp);
+                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO,
+                            SBX_EPILOGUE_NONE, &cfg, &sp);
     if (st != SBX_OK) return st;
     if (sp.split > 1)
         snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);

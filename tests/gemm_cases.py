@@ -58,8 +58,9 @@ def c_window(layout, C, m, n, ldc):
 
 
 def run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-            algo=0, offsets=(0, 0, 0)):
-    """Copy host buffers to the GPU, run sbx_gemm_ex, return the new host C.
+            algo=0, offsets=(0, 0, 0), epilogue=None):
+    """Copy host buffers to the GPU, run sbx_gemm_ex (or sbx_gemm_fused when
+    `epilogue` is given), return the new host C.
 
     `offsets` shifts each device buffer by that many elements (to exercise
     pointers that are not 16-byte aligned)."""
@@ -73,9 +74,15 @@ def run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C,
     dB[offsets[1]:] = torch.from_numpy(B).to(dev)
     dC[offsets[2]:] = torch.from_numpy(C).to(dev)
     es = dA.element_size()
-    sbx.gemm_ex(sbx.F32 if dtype == np.float32 else sbx.F64, layout, ta, tb, m, n, k, alpha,
-                dA.data_ptr() + es * offsets[0], lda, 0, dB.data_ptr() + es * offsets[1], ldb, 0,
-                beta, dC.data_ptr() + es * offsets[2], ldc, 0, 1, algo)
+    ptrs = (dA.data_ptr() + es * offsets[0], dB.data_ptr() + es * offsets[1],
+            dC.data_ptr() + es * offsets[2])
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    if epilogue is None:
+        sbx.gemm_ex(code, layout, ta, tb, m, n, k, alpha, ptrs[0], lda, 0, ptrs[1], ldb, 0,
+                    beta, ptrs[2], ldc, 0, 1, algo)
+    else:
+        sbx.gemm_fused(code, layout, ta, tb, m, n, k, alpha, ptrs[0], lda, 0, ptrs[1], ldb, 0,
+                       beta, ptrs[2], ldc, 0, 1, epilogue)
     torch.cuda.synchronize()
     return dC[offsets[2]:].cpu().numpy()
 

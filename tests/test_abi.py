@@ -105,3 +105,29 @@ def test_huge_leading_dimension_falls_back_to_generic():
     """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
         "generic_64x64x16"
+
+
+def test_fused_gemm_validation():
+    """sbx_gemm_fused validates like sbx_gemm_ex plus the epilogue code."""
+    L = sbx.lib()
+    a = ctypes.c_float(1.0)
+
+    def fused(epilogue, m=4, dtype=0):
+        return L.sbx_gemm_fused(0, dtype, 0, 0, 0, m, 4, 4, ctypes.byref(a), 16, 4, 0, 16, 4, 0,
+                                ctypes.byref(a), 16, 4, 0, 1, epilogue)
+
+    assert fused(2) == 1
+    assert fused(-1) == 1
+    assert fused(1, dtype=7) == 2
+    assert fused(1, m=-1) == 1
+    assert fused(1, m=0) == 0          # no-op, no device needed
+    assert fused(0, m=0) == 0
+
+
+def test_relu_validation():
+    L = sbx.lib()
+    assert L.sbx_relu(0, 7, 16, 4) == 2
+    assert L.sbx_relu(0, 0, 16, -1) == 1
+    assert L.sbx_relu(0, 0, 0, 4) == 1        # null pointer
+    assert L.sbx_relu(0, 1, 12, 4) == 1       # misaligned double
+    assert L.sbx_relu(0, 0, 0, 0) == 0        # empty: no device needed

@@ -276,3 +276,13 @@ def test_checks_catch_a_dropped_beta_term():
     oracle.gemm_naive_ld(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.25, good, ldc)
     oracle.gemm(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, bad, ldc, 1)  # planted: beta lost
     assert oracle.rel_fro_err(bad.reshape(m, n), good.reshape(m, n)) > 1e-3
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_relu_special_values(dtype):
+    """relu.cpp:38-41: greater_than_zero(x) ? x : 0 -- NaN, -0 and -inf map to +0."""
+    x = np.array([1.5, -2.0, 0.0, -0.0, np.inf, -np.inf, np.nan, 1e-300, -1e-300, 3.0], dtype)
+    oracle.relu(x)
+    want = np.array([1.5, 0, 0, 0, np.inf, 0, 0, 1e-300, 0, 3.0], dtype)
+    np.testing.assert_array_equal(x, want)
+    assert not np.signbit(x).any()  # no -0 survives
