@@ -14,8 +14,9 @@ Printed as one JSON line.  Besides the contract fields it carries:
   parity        -- normwise error of the GPU result vs the oracle on the
                    sampled rows (identical input bits)
   also          -- the other BASELINE configs timed the same way (fp64 8192^3,
-                   the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), and
-                   the fused GEMM+ReLU epilogue against GEMM followed by ReLU
+                   the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), the
+                   fused GEMM+ReLU epilogue against GEMM followed by ReLU, GEMV
+                   (HBM GB/s) and SYRK (TFLOP/s over the triangle)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
                        [--cpu-seconds S]
@@ -204,6 +205,58 @@ def run_fused_config(m, n, k, seed, steps, warmup):
     return out
 
 
+def run_gemv_config(dtype, trans, m, n, seed, steps, warmup):
+    """Row-major GEMV y = A x (or A^T x), beta = 0: HBM bound, so reported as
+    GB/s of algorithmic traffic (A once, x once, y written) against 8 TB/s."""
+    import torch
+    import sushiblas_amd as sbx
+    tdt = torch.float32 if dtype == "f32" else torch.float64
+    sdt = sbx.F32 if dtype == "f32" else sbx.F64
+    A = torch.empty(m * n, dtype=tdt, device="cuda")
+    xlen, ylen = (m, n) if trans else (n, m)
+    x = torch.empty(xlen, dtype=tdt, device="cuda")
+    y = torch.zeros(ylen, dtype=tdt, device="cuda")
+    sbx.fill_uniform(A, seed, 0)
+    sbx.fill_uniform(x, seed, 1)
+
+    def step():
+        sbx.gemv(sdt, 0, trans, m, n, 1.0, A, n, x, 1, 0.0, y, 1)
+
+    ms = time_launches(step, steps, warmup)
+    nbytes = (m * n + xlen + ylen) * A.element_size()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"kernel": "gemv_cols" if trans else "gemv_rows", "ms": round(ms, 4),
+           "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "bytes": nbytes}
+    del A, x, y
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_syrk_config(dtype, n, k, seed, steps, warmup):
+    """Row-major SYRK, lower triangle of C = A A^T (A n x k), beta = 0;
+    flops counted as n(n+1)k (the triangle including its diagonal)."""
+    import torch
+    import sushiblas_amd as sbx
+    tdt = torch.float32 if dtype == "f32" else torch.float64
+    sdt = sbx.F32 if dtype == "f32" else sbx.F64
+    A = torch.empty(n * k, dtype=tdt, device="cuda")
+    C = torch.zeros(n * n, dtype=tdt, device="cuda")
+    sbx.fill_uniform(A, seed, 0)
+
+    def step():
+        sbx.syrk(sdt, 0, 0, 0, n, k, 1.0, A, k, 0, 0.0, C, n, 0)
+
+    ms = time_launches(step, steps, warmup)
+    flops = float(n) * (n + 1) * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    out = {"kernel": "mfma triangle tiles", "ms": round(ms, 4), "tflops": round(tflops, 3),
+           "pct_peak": round(100 * tflops / PEAK[dtype], 2)}
+    del A, C
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -298,6 +351,14 @@ def main():
                                                                       steps * 5, 5)
         also["fp32_gemm_relu_8192x8192x256"] = run_fused_config(8192, 8192, 256, SEED + 7,
                                                                 steps * 2, 3)
+        also["fp32_gemv_16384x16384_n"] = run_gemv_config("f32", 0, 16384, 16384, SEED + 8,
+                                                          steps * 2, 3)
+        also["fp32_gemv_16384x16384_t"] = run_gemv_config("f32", 1, 16384, 16384, SEED + 8,
+                                                          steps * 2, 3)
+        also["fp64_gemv_16384x8192_n"] = run_gemv_config("f64", 0, 16384, 8192, SEED + 8,
+                                                         steps * 2, 3)
+        also["fp32_syrk_8192x8192"] = run_syrk_config("f32", 8192, 8192, SEED + 9, steps, 2)
+        also["fp64_syrk_8192x8192"] = run_syrk_config("f64", 8192, 8192, SEED + 9, steps, 2)
         for key, entry in also.items():
             entry["traffic"] = read_traffic(key)
         result["also"] = also

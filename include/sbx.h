@@ -110,6 +110,41 @@ int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, 
  * src/ops/math/nonlinear/relu.cpp:38-41, for FLOAT32/FLOAT64). */
 int sbx_relu(void* stream, int dtype, void* x, int64_t n);
 
+/* GEMV, y = alpha*op(A)*x + beta*y with op(A) = A (m x n) or A^T: replaces
+ * oneapi::mkl::blas::row_major::gemv (src/ops/blas/level2/gemv.cpp:55) and
+ * column_major::gemv (gemv.cpp:60), reached from Level2::gemv (gemv.cpp:65-148)
+ * for FLOAT32 / FLOAT64 (float alpha/beta widened, gemv.cpp:125).  x has
+ * (transA ? m : n) elements x[i*incx], y has (transA ? n : m) elements
+ * y[i*incy]; increments must be positive (the reference passes 1 or a rank-1
+ * tensor's stride, utils.hpp:47-60).  Netlib quick returns: m == 0 or n == 0
+ * leaves y untouched; alpha == 0 gives y = beta*y; beta == 0 never reads y. */
+int sbx_sgemv(void* stream, int layout, int transA, int64_t m, int64_t n, float alpha,
+              const float* A, int64_t lda, const float* x, int64_t incx, float beta, float* y,
+              int64_t incy);
+int sbx_dgemv(void* stream, int layout, int transA, int64_t m, int64_t n, double alpha,
+              const double* A, int64_t lda, const double* x, int64_t incx, double beta,
+              double* y, int64_t incy);
+
+/* SYRK on one triangle of the n x n C: C = alpha*op(A)*op(A)^T + beta*C with
+ * op(A) = A (n x k) when trans == 0 and A^T (A is k x n) when trans == 1;
+ * upper != 0 updates the upper triangle, else the lower; the other triangle
+ * is neither read nor written.  Replaces row_major::syrk / syrk_batch
+ * (src/ops/blas/level3/syrk.cpp:65,60) and column_major::syrk / syrk_batch
+ * (syrk.cpp:78,73), reached from Level3::syrk (syrk.cpp:84-194); batch b uses
+ * A + b*str_a and C + b*str_c.  Quick returns as for GEMM: n == 0 is a
+ * no-op, alpha == 0 or k == 0 gives C = beta*C on the triangle. */
+int sbx_ssyrk(void* stream, int layout, int upper, int trans, int64_t n, int64_t k, float alpha,
+              const float* A, int64_t lda, float beta, float* C, int64_t ldc);
+int sbx_dsyrk(void* stream, int layout, int upper, int trans, int64_t n, int64_t k,
+              double alpha, const double* A, int64_t lda, double beta, double* C, int64_t ldc);
+int sbx_ssyrk_strided_batched(void* stream, int layout, int upper, int trans, int64_t n,
+                              int64_t k, float alpha, const float* A, int64_t lda, int64_t str_a,
+                              float beta, float* C, int64_t ldc, int64_t str_c, int64_t batch);
+int sbx_dsyrk_strided_batched(void* stream, int layout, int upper, int trans, int64_t n,
+                              int64_t k, double alpha, const double* A, int64_t lda,
+                              int64_t str_a, double beta, double* C, int64_t ldc, int64_t str_c,
+                              int64_t batch);
+
 /* Name of the kernel the dispatcher would launch for this problem (tiling
  * heuristics introspection for benchmarks).  Pointers are assumed 16-byte
  * aligned.  Writes a NUL-terminated string of at most cap bytes. */

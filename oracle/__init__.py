@@ -19,5 +19,8 @@ from .sbo import (  # noqa: F401
     fill_uniform,
     fill_normal,
     relu,
+    gemv,
+    syrk,
+    syrk_strided_batched,
     num_threads,
 )

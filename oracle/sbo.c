@@ -273,6 +273,116 @@ void sbo_relu_f64(double* x, int64_t n)
 }
 
 /* ------------------------------------------------------------------------ */
+/* GEMV (gemv.cpp:44-61 -> oneMKL {row,column}_major::gemv).  op(A) is      */
+/* ylen x xlen with ylen = trans ? n : m; each y element is one dot product  */
+/* in double, in index order, then alpha and beta in double and one rounding */
+/* to T.  Netlib quick returns: m == 0 || n == 0 leaves y alone; alpha == 0  */
+/* gives y = beta*y (beta == 0: zeros, y not read).                          */
+/* ------------------------------------------------------------------------ */
+#define DEFINE_GEMV(NAME, T)                                                                      \
+int NAME(int layout, int trans, int64_t m, int64_t n, T alpha, const T* A, int64_t lda,          \
+         const T* x, int64_t incx, T beta, T* y, int64_t incy)                                   \
+{                                                                                                 \
+    if (layout != 0 && layout != 1) return 1;                                                     \
+    if (m < 0 || n < 0 || incx <= 0 || incy <= 0) return 1;                                       \
+    const int64_t need = layout == 0 ? n : m;                                                     \
+    if (lda < (need > 1 ? need : 1)) return 1;                                                    \
+    if (m == 0 || n == 0) return 0;                                                               \
+    const int64_t ylen = trans ? n : m, xlen = trans ? m : n;                                     \
+    if (alpha == (T)0) {                                                                          \
+        if (beta == (T)1) return 0;                                                               \
+        for (int64_t i = 0; i < ylen; ++i)                                                        \
+            y[i * incy] = beta == (T)0 ? (T)0 : (T)((double)beta * (double)y[i * incy]);          \
+        return 0;                                                                                 \
+    }                                                                                             \
+    /* op(A)(i, j) is contiguous along j for row-major A or column-major A^T; */ \
+    /* otherwise along i, and the loops are interchanged over blocks of 256   */ \
+    /* outputs -- each output still sums over j in increasing order.          */ \
+    const int along_j = (layout == 0) == (trans == 0);                                            \
+    _Pragma("omp parallel for schedule(static)")                                                  \
+    for (int64_t i0 = 0; i0 < ylen; i0 += 256) {                                                  \
+        const int64_t i1 = i0 + 256 < ylen ? i0 + 256 : ylen;                                     \
+        double s[256];                                                                            \
+        for (int64_t i = i0; i < i1; ++i) s[i - i0] = 0.0;                                        \
+        if (along_j) {                                                                            \
+            for (int64_t i = i0; i < i1; ++i)                                                     \
+                for (int64_t j = 0; j < xlen; ++j)                                                \
+                    s[i - i0] += (double)A[op_index(layout, trans, i, j, lda)] *                  \
+                                 (double)x[j * incx];                                             \
+        } else {                                                                                  \
+            for (int64_t j = 0; j < xlen; ++j) {                                                  \
+                const double xj = (double)x[j * incx];                                            \
+                for (int64_t i = i0; i < i1; ++i)                                                 \
+                    s[i - i0] += (double)A[op_index(layout, trans, i, j, lda)] * xj;              \
+            }                                                                                     \
+        }                                                                                         \
+        for (int64_t i = i0; i < i1; ++i) {                                                       \
+            double v = (double)alpha * s[i - i0];                                                 \
+            if (beta != (T)0) v += (double)beta * (double)y[i * incy];                            \
+            y[i * incy] = (T)v;                                                                   \
+        }                                                                                         \
+    }                                                                                             \
+    return 0;                                                                                     \
+}
+DEFINE_GEMV(sbo_sgemv, float)
+DEFINE_GEMV(sbo_dgemv, double)
+
+/* ------------------------------------------------------------------------ */
+/* SYRK (syrk.cpp:44-77 -> oneMKL {row,column}_major::syrk[_batch]).  op(A) */
+/* is n x k (trans ? A^T : A); for (i, j) in the requested triangle          */
+/* (upper: j >= i, lower: j <= i) C(i, j) = alpha * sum_l op(A)(i, l)        */
+/* op(A)(j, l) + beta * C(i, j), the sum in double in index order; the other */
+/* triangle is never touched.  alpha == 0 || k == 0: C = beta*C on the      */
+/* triangle; beta == 0: C not read.                                          */
+/* ------------------------------------------------------------------------ */
+#define DEFINE_SYRK(NAME, T)                                                                      \
+int NAME(int layout, int upper, int trans, int64_t n, int64_t k, T alpha, const T* A,            \
+         int64_t lda, int64_t str_a, T beta, T* C, int64_t ldc, int64_t str_c, int64_t batch)    \
+{                                                                                                 \
+    if (layout != 0 && layout != 1) return 1;                                                     \
+    if (n < 0 || k < 0 || batch < 0) return 1;                                                    \
+    const int64_t a_rows = trans ? k : n, a_cols = trans ? n : k;                                 \
+    const int64_t need_a = layout == 0 ? a_cols : a_rows;                                         \
+    if (lda < (need_a > 1 ? need_a : 1) || ldc < (n > 1 ? n : 1)) return 1;                       \
+    const int quick = alpha == (T)0 || k == 0;                                                    \
+    /* op(A) copied into rows of doubles (exact), so every dot product reads */ \
+    /* contiguous memory whatever the layout and transpose                    */ \
+    double* rows = quick || n == 0 ? NULL : (double*)malloc((size_t)n * (size_t)k * sizeof(double)); \
+    if (!quick && n > 0 && !rows) return 2;                                                       \
+    for (int64_t b = 0; b < batch; ++b) {                                                         \
+        const T* a = A + b * str_a;                                                               \
+        T* c = C + b * str_c;                                                                     \
+        if (rows) {                                                                               \
+            _Pragma("omp parallel for schedule(static)")                                          \
+            for (int64_t i = 0; i < n; ++i)                                                       \
+                for (int64_t l = 0; l < k; ++l)                                                   \
+                    rows[i * k + l] = (double)a[op_index(layout, trans, i, l, lda)];              \
+        }                                                                                         \
+        _Pragma("omp parallel for schedule(dynamic, 8)")                                          \
+        for (int64_t i = 0; i < n; ++i) {                                                         \
+            const int64_t j0 = upper ? i : 0, j1 = upper ? n : i + 1;                             \
+            for (int64_t j = j0; j < j1; ++j) {                                                   \
+                T* cp = c + c_index(layout, i, j, ldc);                                           \
+                double v = 0.0;                                                                   \
+                if (!quick) {                                                                     \
+                    const double* ri = rows + i * k;                                              \
+                    const double* rj = rows + j * k;                                              \
+                    double s = 0.0;                                                               \
+                    for (int64_t l = 0; l < k; ++l) s += ri[l] * rj[l];                           \
+                    v = (double)alpha * s;                                                        \
+                }                                                                                 \
+                if (beta != (T)0) v += (double)beta * (double)*cp;                                \
+                *cp = (T)v;                                                                       \
+            }                                                                                     \
+        }                                                                                         \
+    }                                                                                             \
+    free(rows);                                                                                   \
+    return 0;                                                                                     \
+}
+DEFINE_SYRK(sbo_ssyrk_strided_batched, float)
+DEFINE_SYRK(sbo_dsyrk_strided_batched, double)
+
+/* ------------------------------------------------------------------------ */
 /* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).                        */
 /* ------------------------------------------------------------------------ */
 void sbo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])

@@ -18,6 +18,11 @@
  *     this file's own; parity is tolerance-based (normwise relative error).
  *   - sbo_gemm_naive_ld is an independent plain triple loop in long double
  *     over the same element accessors, used to check the blocked routine.
+ *   - sbo_sgemv / sbo_dgemv restate Level2::gemv's oneMKL call
+ *     (src/ops/blas/level2/gemv.cpp:44-61) and sbo_{s,d}syrk_strided_batched
+ *     Level3::syrk's (src/ops/blas/level3/syrk.cpp:44-77): one double dot
+ *     product per output element, netlib quick returns, SYRK touching only
+ *     the requested triangle.
  *   - sbo_philox4x32_10 is the counter-based generator family the reference
  *     uses for its random ops (src/ops/math/random/uniform.cpp:47, oneMKL
  *     philox4x32x10); the algorithm is Salmon et al., "Parallel random
@@ -26,7 +31,8 @@
  *     from this build's own counter mapping, identical on host and device.
  *
  * Pinning (what checks this file): the known answers of
- * tests/blas/level3/test_gemm.cpp:39-88, closed forms from
+ * tests/blas/level3/test_gemm.cpp:39-88, test_syrk.cpp and
+ * tests/blas/level2/test_gemv.cpp, closed forms from
  * tests/runtime/test_framework_sim.cpp, brute force against
  * sbo_gemm_naive_ld, an independent host BLAS (numpy/OpenBLAS and
  * torch/MKL), transpose/column-major invariants, and the published
@@ -78,6 +84,26 @@ double sbo_rel_fro_err_f64(int64_t rows, int64_t cols, const double* X, int64_t 
  * become +0. */
 void sbo_relu_f32(float* x, int64_t n);
 void sbo_relu_f64(double* x, int64_t n);
+
+/* GEMV (src/ops/blas/level2/gemv.cpp:44-61, oneMKL gemv): y = alpha*op(A)*x
+ * + beta*y, A m x n in `layout`, op(A) = A^T when trans; positive
+ * increments.  Dot products in double, one rounding.  Netlib quick returns.
+ * Returns 0, or 1 for invalid arguments. */
+int sbo_sgemv(int layout, int trans, int64_t m, int64_t n, float alpha, const float* A,
+              int64_t lda, const float* x, int64_t incx, float beta, float* y, int64_t incy);
+int sbo_dgemv(int layout, int trans, int64_t m, int64_t n, double alpha, const double* A,
+              int64_t lda, const double* x, int64_t incx, double beta, double* y, int64_t incy);
+
+/* SYRK (src/ops/blas/level3/syrk.cpp:44-77, oneMKL syrk / syrk_batch): the
+ * `upper` (j >= i) or lower (j <= i) triangle of the n x n C becomes
+ * alpha*op(A)*op(A)^T + beta*C, op(A) = A (n x k) or A^T (A k x n); the
+ * other triangle is untouched.  Sums in double, one rounding. */
+int sbo_ssyrk_strided_batched(int layout, int upper, int trans, int64_t n, int64_t k,
+                              float alpha, const float* A, int64_t lda, int64_t str_a,
+                              float beta, float* C, int64_t ldc, int64_t str_c, int64_t batch);
+int sbo_dsyrk_strided_batched(int layout, int upper, int trans, int64_t n, int64_t k,
+                              double alpha, const double* A, int64_t lda, int64_t str_a,
+                              double beta, double* C, int64_t ldc, int64_t str_c, int64_t batch);
 
 /* Philox4x32-10: out[0..3] = philox(ctr[0..3], key[0..1]). */
 void sbo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

@@ -63,6 +63,17 @@ def _load():
         f = getattr(lib, name)
         f.restype = None
         f.argtypes = [_vp, _i64]
+    for name, real in (("sbo_sgemv", ctypes.c_float), ("sbo_dgemv", ctypes.c_double)):
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_int, ctypes.c_int, _i64, _i64, real, _vp, _i64, _vp, _i64, real,
+                      _vp, _i64]
+    for name, real in (("sbo_ssyrk_strided_batched", ctypes.c_float),
+                       ("sbo_dsyrk_strided_batched", ctypes.c_double)):
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _i64, real, _vp, _i64, _i64,
+                      real, _vp, _i64, _i64, _i64]
     lib.sbo_num_threads.restype = ctypes.c_int
     lib.sbo_num_threads.argtypes = []
     _lib = lib
@@ -154,6 +165,38 @@ def relu(x: np.ndarray) -> np.ndarray:
     f = lib.sbo_relu_f32 if x.dtype == np.float32 else lib.sbo_relu_f64
     f(_ptr(x), x.size)
     return x
+
+
+def gemv(layout, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
+    """y <- alpha*op(A)*x + beta*y in place (netlib quick returns)."""
+    lib = _load()
+    if not (A.dtype == x.dtype == y.dtype):
+        raise TypeError("dtype mismatch")
+    f = lib.sbo_sgemv if A.dtype == np.float32 else lib.sbo_dgemv
+    rc = f(int(layout), int(bool(trans)), m, n, float(alpha), _ptr(A), lda, _ptr(x), incx,
+           float(beta), _ptr(y), incy)
+    if rc != 0:
+        raise ValueError(f"oracle gemv rejected its arguments (status {rc})")
+    return y
+
+
+def syrk_strided_batched(layout, upper, trans, n, k, alpha, A, lda, str_a, beta, C, ldc, str_c,
+                         batch):
+    """One triangle of C <- alpha*op(A)*op(A)^T + beta*C, in place."""
+    lib = _load()
+    if A.dtype != C.dtype:
+        raise TypeError("dtype mismatch")
+    f = (lib.sbo_ssyrk_strided_batched if A.dtype == np.float32
+         else lib.sbo_dsyrk_strided_batched)
+    rc = f(int(layout), int(bool(upper)), int(bool(trans)), n, k, float(alpha), _ptr(A), lda,
+           str_a, float(beta), _ptr(C), ldc, str_c, batch)
+    if rc != 0:
+        raise ValueError(f"oracle syrk rejected its arguments (status {rc})")
+    return C
+
+
+def syrk(layout, upper, trans, n, k, alpha, A, lda, beta, C, ldc):
+    return syrk_strided_batched(layout, upper, trans, n, k, alpha, A, lda, 0, beta, C, ldc, 0, 1)
 
 
 def num_threads() -> int:

@@ -70,6 +70,19 @@ def lib() -> ctypes.CDLL:
                                  i64, i64, vp, vp, i64, i64, i64, i32]
     L.sbx_relu.restype = i32
     L.sbx_relu.argtypes = [vp, i32, vp, i64]
+    for name, real in (("sbx_sgemv", ctypes.c_float), ("sbx_dgemv", ctypes.c_double)):
+        f = getattr(L, name)
+        f.restype = i32
+        f.argtypes = [vp, i32, i32, i64, i64, real, vp, i64, vp, i64, real, vp, i64]
+    for name, real in (("sbx_ssyrk_strided_batched", ctypes.c_float),
+                       ("sbx_dsyrk_strided_batched", ctypes.c_double)):
+        f = getattr(L, name)
+        f.restype = i32
+        f.argtypes = [vp, i32, i32, i32, i64, i64, real, vp, i64, i64, real, vp, i64, i64, i64]
+    for name, real in (("sbx_ssyrk", ctypes.c_float), ("sbx_dsyrk", ctypes.c_double)):
+        f = getattr(L, name)
+        f.restype = i32
+        f.argtypes = [vp, i32, i32, i32, i64, i64, real, vp, i64, real, vp, i64]
     L.sbx_gemm_select.restype = i32
     L.sbx_gemm_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64,
                                   ctypes.c_char_p, ctypes.c_size_t]
@@ -158,6 +171,22 @@ def dgemm(layout, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
           stream=None) -> None:
     _check(lib().sbx_dgemm(_stream(stream), int(layout), int(transA), int(transB), m, n, k,
                            alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc), "sbx_dgemm")
+
+
+def gemv(dtype, layout, trans, m, n, alpha, A, lda, x, incx, beta, y, incy,
+         stream=None) -> None:
+    """sbx_sgemv / sbx_dgemv: y = alpha*op(A)*x + beta*y."""
+    f = lib().sbx_sgemv if dtype == F32 else lib().sbx_dgemv
+    _check(f(_stream(stream), int(layout), int(trans), m, n, alpha, _ptr(A), lda, _ptr(x), incx,
+             beta, _ptr(y), incy), "sbx_gemv")
+
+
+def syrk(dtype, layout, upper, trans, n, k, alpha, A, lda, str_a, beta, C, ldc, str_c,
+         batch=1, stream=None) -> None:
+    """sbx_{s,d}syrk_strided_batched: one triangle of C = alpha*op(A)*op(A)^T + beta*C."""
+    f = lib().sbx_ssyrk_strided_batched if dtype == F32 else lib().sbx_dsyrk_strided_batched
+    _check(f(_stream(stream), int(layout), int(upper), int(trans), n, k, alpha, _ptr(A), lda,
+             str_a, beta, _ptr(C), ldc, str_c, batch), "sbx_syrk")
 
 
 def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc) -> str:

@@ -676,6 +676,140 @@ TEST_CASE(ReluNotFusedUnlessSameRegion, true)
     }
 }
 
+// ------------------------------------------------------------- GEMV / SYRK
+
+TEST_CASE(GemvSyrkValidationThrowsAtRecordTime, false)
+{
+    sr::Execution::RuntimeContext local;
+    sb::Engine e(local);
+    sb::Tensor A(nullptr, {2, 3}), x3(nullptr, {3}), y2(nullptr, {2}), v1(nullptr, {3});
+    sb::Tensor m23(nullptr, {2, 3}), y3(nullptr, {3});
+    CHECK_THROWS(e.blas().gemv(v1, x3, y2));             // rank < 2 (gemv.cpp:68)
+    CHECK_THROWS(e.blas().gemv(A, y2, y2));              // x length != n (gemv.cpp:88)
+    CHECK_THROWS(e.blas().gemv(A, x3, y3));              // y length != m (gemv.cpp:89)
+    CHECK_THROWS(e.blas().gemv(A, x3, y3, true));        // transposed: x needs m
+    sb::Tensor xd(nullptr, {3});
+    xd.dtype = DataType::FLOAT64;
+    CHECK_THROWS(e.blas().gemv(A, xd, y2));              // dtype mismatch
+    sb::Tensor xs(nullptr, {3, 1});
+    xs = xs.transpose(0, 1);                             // non-contiguous rank 2 vector
+    CHECK_THROWS(e.blas().gemv(A, xs, y2));
+    sb::Tensor Az(nullptr, {2, 3}), xz(nullptr, {3}), yz(nullptr, {2});
+    Az.dtype = xz.dtype = yz.dtype = DataType::COMPLEX32;
+    CHECK_THROWS(e.blas().gemv(Az, xz, yz));             // not provided
+    sb::Tensor S(nullptr, {3, 2}), Cr(nullptr, {3, 4}), Cs(nullptr, {3, 3}), C2(nullptr, {2, 2});
+    CHECK_THROWS(e.blas().syrk(v1, Cs));                 // rank < 2
+    CHECK_THROWS(e.blas().syrk(S, Cr));                  // C not square (syrk.cpp:96)
+    CHECK_THROWS(e.blas().syrk(S, C2));                  // A rows != n (syrk.cpp:102)
+    CHECK_THROWS(e.blas().syrk(S, Cs, false, true));     // A^T has 2 rows != 3
+    sb::Tensor Sh(nullptr, {3, 2}), Ch(nullptr, {3, 3});
+    Sh.dtype = Ch.dtype = DataType::HALF;
+    CHECK_THROWS(e.blas().syrk(Sh, Ch));
+    CHECK(e.get_graph().pending() == 0);
+}
+
+TEST_CASE(SimpleGEMV, true)  // tests/blas/level2/test_gemv.cpp
+{
+    sb::Engine engine(ctx());
+    auto A = engine.create_tensor({2, 3});
+    auto X = engine.create_tensor({3});
+    auto Y = engine.create_tensor({2});
+    fill_tensor(A, {1, 2, 3, 4, 5, 6});
+    fill_tensor(X, {1, 1, 1});
+    fill_tensor(Y, {0, 0});
+    engine.blas().gemv(A, X, Y);
+    engine.execute().wait();
+    verify_tensor(Y, {6, 15}, 0.0);
+}
+
+TEST_CASE(SimpleSYRK, true)  // tests/blas/level3/test_syrk.cpp
+{
+    sb::Engine engine(ctx());
+    auto A = engine.create_tensor({3, 2});
+    auto C = engine.create_tensor({3, 3});
+    fill_tensor(A, {1, 2, 3, 4, 5, 6});
+    fill_tensor(C, std::vector<float>(9, 0.0f));
+    engine.blas().syrk(A, C, false, false, 1.0f, 0.0f);
+    engine.execute().wait();
+    verify_tensor(C, {5, 0, 0, 11, 25, 0, 17, 39, 61}, 0.0);
+}
+
+TEST_CASE(SimpleSYRKColumnMajor, true)  // tests/blas/level3/test_syrk.cpp
+{
+    sb::Engine engine(ctx(), Layout::COLUMN_MAJOR);
+    auto A = engine.create_tensor({3, 2});  // transA: A is K x N
+    auto C = engine.create_tensor({2, 2});
+    fill_tensor(A, {1, 2, 3, 4, 5, 6});
+    fill_tensor(C, std::vector<float>(4, 0.0f));
+    engine.blas().syrk(A, C, false, true, 1.0f, 0.0f);
+    engine.execute().wait();
+    verify_tensor(C, {14, 32, 0, 77}, 0.0);
+}
+
+TEST_CASE(GemvTransposedStridedFp64, true)
+{
+    // y (n) = 0.5 * A^T x + 2 y with x a rank-1 view of stride 3, fp64
+    sb::Engine engine(ctx());
+    const int m = 37, n = 29;
+    auto A = engine.create_tensor({m, n}, DataType::FLOAT64);
+    auto Xbuf = engine.create_tensor({3 * m}, DataType::FLOAT64);
+    auto Y = engine.create_tensor({n}, DataType::FLOAT64);
+    std::vector<double> a(m * n), xb(3 * m), y(n);
+    for (int i = 0; i < m * n; ++i) a[i] = std::sin(0.1 * i);
+    for (int i = 0; i < 3 * m; ++i) xb[i] = std::cos(0.2 * i);
+    for (int i = 0; i < n; ++i) y[i] = 0.125 * i;
+    fill_tensor<double>(A, a);
+    fill_tensor<double>(Xbuf, xb);
+    fill_tensor<double>(Y, y);
+    sb::Tensor X = Xbuf;  // the view x[i] = xb[3 i]
+    X.shape[0] = m;
+    X.num_elements = m;
+    X.strides[0] = 3;
+    engine.blas().gemv(A, X, Y, true, 0.5f, 2.0f);
+    engine.execute().wait();
+    const double* got = Y.data_as<double>();
+    for (int j = 0; j < n; ++j)
+    {
+        double s = 0;
+        for (int i = 0; i < m; ++i) s += a[i * n + j] * xb[3 * i];
+        CHECK_NEAR(got[j], 0.5 * s + 2.0 * y[j], 1e-13);
+    }
+}
+
+TEST_CASE(SyrkBatchedUpperMatchesHostLoop, true)
+{
+    // rank-3: 3 problems of C (40x40) = A (40x17) A^T, upper triangle, beta = 1
+    sb::Engine engine(ctx());
+    const int b = 3, n = 40, k = 17;
+    auto A = engine.create_tensor({b, n, k});
+    auto C = engine.create_tensor({b, n, n});
+    std::vector<float> a(b * n * k), c(b * n * n);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = std::sin(0.3f * i);
+    for (size_t i = 0; i < c.size(); ++i) c[i] = 0.5f * ((i % 7) - 3);
+    fill_tensor(A, a);
+    fill_tensor(C, c);
+    std::vector<std::string> names;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
+    engine.blas().syrk(A, C, true, false, 1.0f, 1.0f);
+    engine.execute().wait();
+    CHECK(names.size() == 1 && names[0] == "blas.lvl3.syrk");
+    const float* got = C.data_as<float>();
+    for (int q = 0; q < b; ++q)
+        for (int i = 0; i < n; ++i)
+            for (int j = 0; j < n; ++j)
+            {
+                const int idx = q * n * n + i * n + j;
+                if (j < i)
+                {
+                    CHECK(got[idx] == c[idx]);  // lower triangle untouched
+                    continue;
+                }
+                double s = 0;
+                for (int l = 0; l < k; ++l) s += double(a[(q * n + i) * k + l]) * a[(q * n + j) * k + l];
+                CHECK_NEAR(got[idx], s + c[idx], 1e-4);
+            }
+}
+
 TEST_CASE(LargeFp32MatchesHostLoop, true)
 {
     // 300 x 257 x 129 with odd leading dimensions, against a double host loop

@@ -25,6 +25,8 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs<T> p)
     const int tid = threadIdx.x;
     const int tx = tid & 15, ty = tid >> 4;
     const int tm = blockIdx.x % p.tiles_m, tn = blockIdx.x / p.tiles_m;
+    // a triangle (SYRK) skips the tiles wholly outside it
+    if ((p.uplo == 1 && tn > tm) || (p.uplo == 2 && tn < tm)) return;
     const int64_t m0 = (int64_t)tm * 64, n0 = (int64_t)tn * 64;
     const int64_t bz = blockIdx.z;
     const T* A = p.A + bz * p.str_a;
@@ -77,7 +79,8 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs<T> p)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t m = m0 + ty + 16 * i, n = n0 + tx + 16 * j;
-            if (m < p.M && n < p.N) {
+            const bool in_tri = p.uplo == 0 || (p.uplo == 1 ? n <= m : n >= m);
+            if (m < p.M && n < p.N && in_tri) {
                 T* cp = C + m * p.ldc + n;
                 T v = p.alpha * acc[i][j];
                 if (read_c) v += p.beta * *cp;
@@ -107,17 +110,19 @@ template hipError_t launch_generic<double>(const GemmArgs<double>&, bool, bool, 
                                            hipStream_t);
 
 // ---------------------------------------------------------------------------
-// C <- beta*C over an m x n row-major window (then the ReLU when fused).
+// C <- beta*C over an m x n row-major window (then the ReLU when fused);
+// uplo 1 / 2 restricts it to the lower / upper triangle (SYRK's quick return).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t str_c, int64_t m,
-                                                    int64_t n, T beta, int relu)
+                                                    int64_t n, T beta, int relu, int uplo)
 {
     T* c = C + (int64_t)blockIdx.z * str_c;
     const int64_t total = m * n;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * 256) {
         const int64_t i = e / n, j = e - i * n;
+        if ((uplo == 1 && j > i) || (uplo == 2 && j < i)) continue;
         T* cp = c + i * ldc + j;
         const T v = beta == (T)0 ? (T)0 : beta * *cp;
         *cp = relu ? relu_of(v) : v;
@@ -126,20 +131,20 @@ __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t s
 
 template <typename T>
 hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
-                        int relu, int batch, hipStream_t stream)
+                        int relu, int uplo, int batch, hipStream_t stream)
 {
     int64_t blocks = (m * n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     if (blocks < 1) blocks = 1;
     scale_kernel<T><<<dim3((unsigned)blocks, 1, (unsigned)batch), dim3(256), 0, stream>>>(
-        C, ldc, str_c, m, n, beta, relu);
+        C, ldc, str_c, m, n, beta, relu, uplo);
     return hipGetLastError();
 }
 
 template hipError_t launch_scale<float>(float*, int64_t, int64_t, int64_t, int64_t, float, int,
-                                        int, hipStream_t);
+                                        int, int, hipStream_t);
 template hipError_t launch_scale<double>(double*, int64_t, int64_t, int64_t, int64_t, double,
-                                         int, int, hipStream_t);
+                                         int, int, int, hipStream_t);
 
 // ---------------------------------------------------------------------------
 // Elementwise ReLU over n contiguous elements (the stand-alone form of the

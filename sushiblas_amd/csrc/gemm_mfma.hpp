@@ -30,6 +30,9 @@
 //    (hardware deals workgroups round-robin over the 8 XCDs) and, inside an
 //    XCD, walk a GROUP_M-tall column of tiles so that A row-panels and B
 //    column-panels are shared through that XCD's L2.
+//  * SYRK (src/ops/blas/level3/syrk.cpp:84-194) runs through the same kernel
+//    with B = A and `uplo` set: only the tiles that meet the requested
+//    triangle are enumerated, and diagonal tiles store only the triangle.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -183,7 +186,37 @@ struct GemmArgs {
     int split;
     T* ws;
     int relu;  // 1: C = max(alpha*A*B + beta*C, 0) with NaN -> 0 (fused ReLU epilogue)
+    // Triangle-only output (SYRK): 0 = whole C; 1 = lower (column <= row);
+    // 2 = upper (column >= row).  With uplo != 0, BM == BN, tiles_m ==
+    // tiles_n = T and only the T(T+1)/2 tiles that meet the triangle exist.
+    int uplo;
+    int tiles;  // tiles in the grid: tiles_m * tiles_n, or T(T+1)/2 for a triangle
 };
+
+// Tile id -> (tile row, tile column).  Whole C: GROUP_M-tall column walk, so
+// consecutive ids share B column panels and a group's A row panels.  Triangle:
+// row-by-row over the lower triangle (row r holds tiles 0..r), mirrored for
+// upper, so consecutive ids share the A row panel.
+template <typename T>
+__device__ inline void tile_coords(const GemmArgs<T>& p, int id, int& tm, int& tn)
+{
+    if (p.uplo == 0) {
+        const int group_span = p.group_m * p.tiles_n;
+        const int group = id / group_span;
+        const int first_m = group * p.group_m;
+        const int gsize = min(p.tiles_m - first_m, p.group_m);
+        const int in_group = id - group * group_span;
+        tm = first_m + in_group % gsize;
+        tn = in_group / gsize;
+        return;
+    }
+    int r = (int)((sqrtf(8.0f * (float)id + 1.0f) - 1.0f) * 0.5f);
+    while (r > 0 && r * (r + 1) / 2 > id) --r;
+    while ((r + 1) * (r + 2) / 2 <= id) ++r;
+    const int c = id - r * (r + 1) / 2;
+    if (p.uplo == 1) { tm = r; tn = c; }
+    else { tm = c; tn = r; }
+}
 
 // The reference's ReLU: x > 0 ? x : 0 (NaN and -0 become +0).
 template <typename T>
@@ -390,13 +423,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
         const int per_xcd = p.num_full >> 3;
         id = (id & 7) * per_xcd + (id >> 3);
     }
-    const int group_span = p.group_m * p.tiles_n;
-    const int group = id / group_span;
-    const int first_m = group * p.group_m;
-    const int gsize = min(p.tiles_m - first_m, p.group_m);
-    const int in_group = id - group * group_span;
-    const int tm = first_m + in_group % gsize;
-    const int tn = in_group / gsize;
+    int tm, tn;
+    tile_coords(p, id, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int64_t bz = blockIdx.z;
@@ -483,7 +511,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // next part's data) and what they write to the idle LDS buffer is unused.
     auto step = [&](auto S, int kt, int cur) {
         constexpr int st = decltype(S)::value;
-        if (PF == 1) issue(Int<0>{}, kt + 1);
+        if constexpr (PF == 1) issue(Int<0>{}, kt + 1);
         else issue(Int<st ^ 1>{}, kt + 2);
 #pragma unroll
         for (int g = 0; g + 1 < G; ++g) {
@@ -532,7 +560,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     };
 
     // prologue: tile kt0 -> LDS buffer 0 (and tile kt0+1 -> staging set 0 if PF == 2)
-    if (PF == 1) {
+    if constexpr (PF == 1) {
         issue(Int<0>{}, kt0);
         commit(Int<0>{}, 0);
     } else {
@@ -543,7 +571,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
 
-    if (PF == 1) {
+    if constexpr (PF == 1) {
         for (int kt = kt0; kt < nk; ++kt) step(Int<0>{}, kt, (kt - kt0) & 1);
     } else {
         for (int kt = kt0; kt < nk; kt += 2) {
@@ -566,6 +594,9 @@ gemm_mfma_kernel(GemmArgs<T> p)
     T alpha, beta;
     bool vec_ok;
     bool relu = false;
+    // triangle window of a row: columns [m + lo_off, m + hi_off] of the tile
+    // stay (local column c of local row m is global column n0 + c, row m0 + m)
+    int lo_off = -(1 << 30), hi_off = 1 << 30;
     if (is_split) {
         dst = p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN);
         ldd = BN;
@@ -583,6 +614,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
         beta = p.beta;
         vec_ok = p.c_vec;
         relu = p.relu != 0;
+        if (p.uplo == 1) hi_off = m0 - n0;       // column <= row
+        else if (p.uplo == 2) lo_off = m0 - n0;  // column >= row
     }
     const bool read_c = beta != (T)0;
 #pragma unroll
@@ -590,11 +623,13 @@ gemm_mfma_kernel(GemmArgs<T> p)
 #pragma unroll
         for (int s = 0; s < NBN / UB; ++s) {
             const int nb = wn0 + FragB::map(s * UB, jl);
-            const bool vec = UB > 1 && vec_ok && nb + UB <= col_lim;
 #pragma unroll
             for (int r = 0; r < MF::NACC; ++r) {
                 const int m = wm0 + FragA::map(i, MF::row(r, q));
                 if (m >= row_lim) continue;
+                const int c_lo = max(0, m + lo_off);
+                const int c_hi = min(col_lim, m + hi_off + 1);
+                const bool vec = UB > 1 && vec_ok && nb >= c_lo && nb + UB <= c_hi;
                 T* cp = dst + (int64_t)m * ldd + nb;
                 T v[UB];
 #pragma unroll
@@ -614,7 +649,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
                 } else {
 #pragma unroll
                     for (int u = 0; u < UB; ++u)
-                        if (nb + u < col_lim) {
+                        if (nb + u >= c_lo && nb + u < c_hi) {
                             T w = v[u];
                             if (read_c) w += beta * cp[u];
                             cp[u] = relu ? relu_of(w) : w;
@@ -626,7 +661,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
 
 // Split-K finish: for tail tile `slot` (tile id num_full + slot), sum the
 // `split` partials in part order (deterministic), then C = alpha*sum + beta*C
-// (and the ReLU when fused).
+// (and the ReLU when fused); for a triangle, only the triangle's elements.
 // One lane per element, one workgroup of 256 lanes per (slot, 256-element
 // chunk); all of a lane's partial loads are issued before the sum.
 constexpr int kMaxSplitParts = 8;
@@ -637,16 +672,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
     constexpr int CHUNKS = BM * BN / 256;
     const int slot = blockIdx.x / CHUNKS;
     const int chunk = blockIdx.x - slot * CHUNKS;
-    const int id = p.num_full + slot;
-    const int group_span = p.group_m * p.tiles_n;
-    const int group = id / group_span;
-    const int first_m = group * p.group_m;
-    const int gsize = min(p.tiles_m - first_m, p.group_m);
-    const int in_group = id - group * group_span;
+    int tm, tn;
+    tile_coords(p, p.num_full + slot, tm, tn);
     const int e = chunk * 256 + threadIdx.x;
-    const int m = (first_m + in_group % gsize) * BM + e / BN;
-    const int n = (in_group / gsize) * BN + e % BN;
+    const int m = tm * BM + e / BN;
+    const int n = tn * BN + e % BN;
     if (m >= p.M || n >= p.N) return;
+    if ((p.uplo == 1 && n > m) || (p.uplo == 2 && n < m)) return;
     const T* part0 = p.ws + (int64_t)slot * p.split * (BM * BN) + e;
     T v[kMaxSplitParts];
 #pragma unroll

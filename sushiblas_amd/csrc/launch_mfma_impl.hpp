@@ -13,7 +13,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, b
                        int batch, hipStream_t stream)
 {
     constexpr int V = 16 / (int)sizeof(T);
-    const int tiles = a.tiles_m * a.tiles_n;
+    const int tiles = a.tiles;
     const dim3 grid((unsigned)(a.num_full + (tiles - a.num_full) * a.split), 1, (unsigned)batch);
     const dim3 block(256);
     const int sel = (a_kc ? 8 : 0) | (b_kc ? 4 : 0) | (a_vec ? 2 : 0) | (b_vec ? 1 : 0);

@@ -14,6 +14,7 @@
 #include <utility>
 
 #include "../../include/sbx.h"
+#include "gemv.hpp"
 #include "launch.hpp"
 
 namespace sbx {
@@ -40,6 +41,7 @@ struct Problem {
     int64_t ldc, str_c;
     int64_t batch;
     int relu;  // fused ReLU epilogue
+    int uplo;  // 0: whole C; 1 / 2: lower / upper triangle only (SYRK, B == A, m == n)
 };
 
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
@@ -69,8 +71,14 @@ const CfgInfo kCfg[] = {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-Cfg choose_cfg(int dtype, int64_t m, int64_t n)
+Cfg choose_cfg(int dtype, int64_t m, int64_t n, int uplo = 0)
 {
+    if (uplo) {
+        // a triangle needs square tiles, so diagonal tiles are the tm == tn ones
+        if (dtype != SBX_F32) return F64_128x128;
+        const int64_t t = cdiv(n, 256);
+        return t * (t + 1) / 2 >= 256 ? F32_256x256 : F32_128x128;
+    }
     if (dtype == SBX_F32) {
         if (n <= 64) return F32_128x64;
         if (m <= 64) return F32_64x128;
@@ -253,14 +261,15 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
-    Cfg cfg = choose_cfg(p.dtype, p.m, p.n);
+    Cfg cfg = choose_cfg(p.dtype, p.m, p.n, p.uplo);
     if (algo == SBX_ALGO_GENERIC) cfg = GENERIC;
     if (cfg != GENERIC && !mfma_feasible(p, cfg)) {
         if (algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
         cfg = GENERIC;
     }
     const CfgInfo& info = kCfg[cfg];
-    const int64_t tiles = cdiv(p.m, info.bm) * cdiv(p.n, info.bn);
+    const int64_t tiles = p.uplo ? cdiv(p.n, info.bn) * (cdiv(p.n, info.bn) + 1) / 2
+                                 : cdiv(p.m, info.bm) * cdiv(p.n, info.bn);
     SplitPlan sp{(int)tiles, 1, 0};
     if (cfg != GENERIC && !quick)
         sp = plan_split(tiles, (int64_t)cu_count() * info.per_cu, cdiv(p.k, info.bk), p.batch);
@@ -279,7 +288,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         hipError_t e;
         if (quick) {
             e = launch_scale<T>((T*)p.C + b0 * p.str_c, p.ldc, p.str_c, p.m, p.n, beta, p.relu,
-                                nb, stream);
+                                p.uplo, nb, stream);
         } else {
             GemmArgs<T> a;
             a.A = (const T*)p.A + b0 * p.str_a;
@@ -299,6 +308,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.split = sp.split;
             a.ws = (T*)ws;
             a.relu = p.relu;
+            a.uplo = p.uplo;
+            a.tiles = (int)tiles;
             const size_t elem = sizeof(T);
             const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
                                                 a.A, elem);
@@ -355,6 +366,7 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     }
     p.k = k; p.C = C; p.ldc = ldc; p.str_c = batch > 1 ? str_c : 0; p.batch = batch;
     p.relu = epilogue == SBX_EPILOGUE_RELU;
+    p.uplo = 0;
     if (batch <= 1) { p.str_a = 0; p.str_b = 0; }
 
     hipStream_t s = (hipStream_t)stream;
@@ -363,6 +375,119 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
                           chosen_split);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
                        chosen_split);
+}
+
+// SYRK: C = alpha * op(A) op(A)^T + beta * C on one triangle of the n x n C
+// (the arithmetic of oneMKL's syrk / syrk_batch, syrk.cpp:44-77), run as a
+// GEMM with B = A whose tile grid covers only that triangle.  Row-major:
+// trans == 0 is A (n x k) times A^T, trans == 1 is A^T A with A k x n.  A
+// column-major call is the row-major one on the same memory with `upper` and
+// `trans` flipped (column-major C's lower triangle is row-major C^T's upper,
+// and a column-major n x k A is a row-major k x n one).
+int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
+              const void* alpha, const void* A, int64_t lda, int64_t str_a, const void* beta,
+              void* C, int64_t ldc, int64_t str_c, int64_t batch)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
+    if ((upper != 0 && upper != 1) || (trans != 0 && trans != 1)) return SBX_INVALID_ARGUMENT;
+    if (n < 0 || k < 0 || batch < 0) return SBX_INVALID_ARGUMENT;
+    if (n > kMaxDim || k > kMaxDim) return SBX_UNSUPPORTED;
+    if (!alpha || !beta) return SBX_INVALID_ARGUMENT;
+    if (check_ld(layout, trans, n, k, lda) || check_ld(layout, false, n, n, ldc))
+        return SBX_INVALID_ARGUMENT;
+    if (batch > 1 && (str_a < 0 || str_c <= 0)) return SBX_INVALID_ARGUMENT;
+    const size_t elem = dtype == SBX_F32 ? 4 : 8;
+    const bool alpha0 = dtype == SBX_F32 ? *(const float*)alpha == 0.0f
+                                         : *(const double*)alpha == 0.0;
+    if (n > 0 && batch > 0) {
+        if (!C || (uintptr_t)C % elem) return SBX_INVALID_ARGUMENT;
+        if (k > 0 && !alpha0 && (!A || (uintptr_t)A % elem)) return SBX_INVALID_ARGUMENT;
+    }
+    const int up = layout == 0 ? upper : !upper;
+    const int tr = layout == 0 ? trans : !trans;
+    Problem p;
+    p.dtype = dtype;
+    p.ta = tr;
+    p.tb = !tr;
+    p.m = n; p.n = n; p.k = k;
+    p.A = A; p.lda = lda; p.str_a = batch > 1 ? str_a : 0;
+    p.B = A; p.ldb = lda; p.str_b = p.str_a;
+    p.C = C; p.ldc = ldc; p.str_c = batch > 1 ? str_c : 0;
+    p.batch = batch;
+    p.relu = 0;
+    p.uplo = up ? 2 : 1;
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SBX_F32)
+        return run<float>(p, *(const float*)alpha, *(const float*)beta, SBX_ALGO_AUTO, s,
+                          nullptr, nullptr);
+    return run<double>(p, *(const double*)alpha, *(const double*)beta, SBX_ALGO_AUTO, s,
+                       nullptr, nullptr);
+}
+
+// GEMV: y = alpha * op(A) x + beta * y (oneMKL gemv, gemv.cpp:44-61), netlib
+// quick returns: m == 0 or n == 0 leaves y untouched; alpha == 0 gives
+// y = beta * y (zeros when beta == 0, y not read).  A column-major m x n A is
+// a row-major n x m A^T, so the transpose flag flips.
+template <typename T>
+int gemv_run(hipStream_t stream, bool trans, int64_t rows, int64_t cols, T alpha, const T* A,
+             int64_t lda, const T* x, int64_t incx, T beta, T* y, int64_t incy)
+{
+    const int64_t ylen = trans ? cols : rows;
+    if (alpha == (T)0) {
+        if (beta == (T)1) return SBX_OK;
+        // y as a ylen x 1 matrix with row pitch incy
+        return launch_scale<T>(y, incy, 0, ylen, 1, beta, 0, 0, 1, stream) == hipSuccess
+                   ? SBX_OK : SBX_HIP_ERROR;
+    }
+    constexpr int64_t V = 16 / (int64_t)sizeof(T);
+    const bool a_vec = (uintptr_t)A % 16 == 0 && lda % V == 0;
+    const bool vec = trans ? a_vec : (a_vec && incx == 1 && (uintptr_t)x % 16 == 0);
+    GemvPlan pl = plan_gemv<T>(trans, rows, cols, vec, cu_count());
+    GemvArgs<T> a;
+    a.A = A; a.x = x; a.y = y;
+    a.lda = lda; a.incx = incx; a.incy = incy;
+    a.rows = rows; a.cols = cols;
+    a.alpha = alpha; a.beta = beta;
+    a.cw = pl.cw;
+    a.ws = nullptr;
+    if (pl.chunks > 1) {
+        a.ws = (T*)stream_workspace(stream, (size_t)pl.chunks * pl.out_len * sizeof(T));
+        if (!a.ws) {  // no memory for partials: one range
+            pl.chunks = 1;
+            pl.cw = trans ? rows : cols;
+        }
+    }
+    return launch_gemv<T>(a, pl, stream) == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
+}
+
+int gemv_impl(void* stream, int dtype, int layout, int trans, int64_t m, int64_t n,
+              const void* alpha, const void* A, int64_t lda, const void* x, int64_t incx,
+              const void* beta, void* y, int64_t incy)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
+    if (trans != 0 && trans != 1) return SBX_INVALID_ARGUMENT;
+    if (m < 0 || n < 0) return SBX_INVALID_ARGUMENT;
+    if (incx == 0 || incy == 0) return SBX_INVALID_ARGUMENT;
+    if (incx < 0 || incy < 0) return SBX_UNSUPPORTED;
+    if (!alpha || !beta) return SBX_INVALID_ARGUMENT;
+    if (check_ld(layout, false, m, n, lda)) return SBX_INVALID_ARGUMENT;
+    if (m == 0 || n == 0) return SBX_OK;
+    const size_t elem = dtype == SBX_F32 ? 4 : 8;
+    const bool alpha0 = dtype == SBX_F32 ? *(const float*)alpha == 0.0f
+                                         : *(const double*)alpha == 0.0;
+    if (!y || (uintptr_t)y % elem) return SBX_INVALID_ARGUMENT;
+    if (!alpha0 && (!A || !x || (uintptr_t)A % elem || (uintptr_t)x % elem))
+        return SBX_INVALID_ARGUMENT;
+    const bool t = layout == 0 ? trans != 0 : trans == 0;
+    const int64_t rows = layout == 0 ? m : n, cols = layout == 0 ? n : m;
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SBX_F32)
+        return gemv_run<float>(s, t, rows, cols, *(const float*)alpha, (const float*)A, lda,
+                               (const float*)x, incx, *(const float*)beta, (float*)y, incy);
+    return gemv_run<double>(s, t, rows, cols, *(const double*)alpha, (const double*)A, lda,
+                            (const double*)x, incx, *(const double*)beta, (double*)y, incy);
 }
 
 }  // namespace
@@ -402,6 +527,57 @@ int sbx_relu(void* stream, int dtype, void* x, int64_t n)
         ? sbx::launch_relu<float>((float*)x, n, (hipStream_t)stream)
         : sbx::launch_relu<double>((double*)x, n, (hipStream_t)stream);
     return e == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
+}
+
+int sbx_sgemv(void* stream, int layout, int transA, int64_t m, int64_t n, float alpha,
+              const float* A, int64_t lda, const float* x, int64_t incx, float beta, float* y,
+              int64_t incy)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::gemv_impl(stream, SBX_F32, layout, transA, m, n, &alpha, A, lda, x, incx, &beta,
+                          y, incy);
+}
+
+int sbx_dgemv(void* stream, int layout, int transA, int64_t m, int64_t n, double alpha,
+              const double* A, int64_t lda, const double* x, int64_t incx, double beta,
+              double* y, int64_t incy)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::gemv_impl(stream, SBX_F64, layout, transA, m, n, &alpha, A, lda, x, incx, &beta,
+                          y, incy);
+}
+
+int sbx_ssyrk_strided_batched(void* stream, int layout, int upper, int trans, int64_t n,
+                              int64_t k, float alpha, const float* A, int64_t lda, int64_t str_a,
+                              float beta, float* C, int64_t ldc, int64_t str_c, int64_t batch)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::syrk_impl(stream, SBX_F32, layout, upper, trans, n, k, &alpha, A, lda, str_a,
+                          &beta, C, ldc, str_c, batch);
+}
+
+int sbx_dsyrk_strided_batched(void* stream, int layout, int upper, int trans, int64_t n,
+                              int64_t k, double alpha, const double* A, int64_t lda,
+                              int64_t str_a, double beta, double* C, int64_t ldc, int64_t str_c,
+                              int64_t batch)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::syrk_impl(stream, SBX_F64, layout, upper, trans, n, k, &alpha, A, lda, str_a,
+                          &beta, C, ldc, str_c, batch);
+}
+
+int sbx_ssyrk(void* stream, int layout, int upper, int trans, int64_t n, int64_t k, float alpha,
+              const float* A, int64_t lda, float beta, float* C, int64_t ldc)
+{
+    return sbx_ssyrk_strided_batched(stream, layout, upper, trans, n, k, alpha, A, lda, 0, beta,
+                                     C, ldc, 0, 1);
+}
+
+int sbx_dsyrk(void* stream, int layout, int upper, int trans, int64_t n, int64_t k,
+              double alpha, const double* A, int64_t lda, double beta, double* C, int64_t ldc)
+{
+    return sbx_dsyrk_strided_batched(stream, layout, upper, trans, n, k, alpha, A, lda, 0, beta,
+                                     C, ldc, 0, 1);
 }
 
 int sbx_sgemm(void* stream, int layout, int transA, int transB, int64_t m, int64_t n, int64_t k,

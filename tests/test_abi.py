@@ -131,3 +131,44 @@ def test_relu_validation():
     assert L.sbx_relu(0, 0, 0, 4) == 1        # null pointer
     assert L.sbx_relu(0, 1, 12, 4) == 1       # misaligned double
     assert L.sbx_relu(0, 0, 0, 0) == 0        # empty: no device needed
+
+
+def test_gemv_validation():
+    """sbx_sgemv rejects bad arguments on the host; m == 0 / n == 0 need no device."""
+    L = sbx.lib()
+
+    def gemv(layout=0, trans=0, m=4, n=4, A=16, lda=4, x=16, incx=1, y=16, incy=1):
+        return L.sbx_sgemv(0, layout, trans, m, n, 1.0, A, lda, x, incx, 0.0, y, incy)
+
+    assert gemv(layout=2) == 1
+    assert gemv(trans=3) == 1
+    assert gemv(m=-1) == 1
+    assert gemv(lda=3) == 1                 # row-major: lda >= n
+    assert gemv(layout=1, m=8, lda=4) == 1  # column-major: lda >= m
+    assert gemv(incx=0) == 1
+    assert gemv(incy=-1) == 2               # negative increments are not provided
+    assert gemv(y=0) == 1
+    assert gemv(x=0) == 1
+    assert gemv(A=18) == 1                  # misaligned
+    assert gemv(m=0) == 0 and gemv(n=0) == 0
+
+
+def test_syrk_validation():
+    L = sbx.lib()
+
+    def syrk(layout=0, upper=0, trans=0, n=4, k=4, A=16, lda=4, sa=0, C=16, ldc=4, sc=0,
+             batch=1):
+        return L.sbx_ssyrk_strided_batched(0, layout, upper, trans, n, k, 1.0, A, lda, sa, 0.0,
+                                           C, ldc, sc, batch)
+
+    assert syrk(layout=2) == 1
+    assert syrk(upper=2) == 1
+    assert syrk(trans=-1) == 1
+    assert syrk(n=-1) == 1
+    assert syrk(lda=3) == 1
+    assert syrk(trans=1, n=8, lda=4, ldc=8) == 1       # A k x n row-major: lda >= n
+    assert syrk(ldc=3) == 1
+    assert syrk(C=0) == 1
+    assert syrk(batch=2, sc=0) == 1
+    assert syrk(n=0) == 0 and syrk(batch=0) == 0
+    assert syrk(n=1 << 31) == 2
