@@ -19,7 +19,9 @@ Printed as one JSON line.  Besides the contract fields it carries:
                    (HBM GB/s) and SYRK (TFLOP/s over the triangle)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
-                       [--cpu-seconds S]
+                       [--cpu-seconds S] [--no-cpu]
+       python bench.py --only <also key>     (one secondary workload, for profiling)
+       python bench.py --calibrate-copy      (1 GiB copy, the PMC byte reference)
 """
 import argparse
 import json
@@ -45,6 +47,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--only", default=None,
+                    help="run one secondary workload (a key of the `also` object) and print "
+                         "it alone: one workload per run for rocprofv3 counter passes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (torch copy_) a few "
                          "times: the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -257,6 +262,39 @@ def run_syrk_config(dtype, n, k, seed, steps, warmup):
     return out
 
 
+def secondary_workloads(steps_arg):
+    """The `also` workloads in run order, as key -> thunk."""
+    steps = max(3, min(steps_arg, 10))
+    w = {}
+    w["fp64_8192_cfg5"] = lambda: run_config("f64", 0, 0, 0, 8192, 8192, 8192, 1.0, 0.0,
+                                             SEED + 5, steps, 2)
+    for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+        w[f"fp32_ragged_cfg3_t{ta}{tb}"] = (lambda ta=ta, tb=tb: run_config(
+            "f32", 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3, steps, 2))
+
+    def tall_skinny():
+        ts = run_config("f32", 0, 0, 0, 65536, 64, 4096, 1.0, 0.0, SEED + 4, steps, 2,
+                        dist="tall_skinny")
+        ts["hbm_frac"] = round(ts["hbm_gbs"] / HBM_PEAK_GBS, 4)
+        return ts
+    w["fp32_tall_skinny_cfg4"] = tall_skinny
+    w["fp32_512_cfg1"] = lambda: run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
+                                            steps * 5, 5)
+    w["fp32_gemm_relu_layer_512x1024x1024"] = lambda: run_fused_config(
+        512, 1024, 1024, SEED + 6, steps * 5, 5)
+    w["fp32_gemm_relu_8192x8192x256"] = lambda: run_fused_config(8192, 8192, 256, SEED + 7,
+                                                                 steps * 2, 3)
+    w["fp32_gemv_16384x16384_n"] = lambda: run_gemv_config("f32", 0, 16384, 16384, SEED + 8,
+                                                           steps * 2, 3)
+    w["fp32_gemv_16384x16384_t"] = lambda: run_gemv_config("f32", 1, 16384, 16384, SEED + 8,
+                                                           steps * 2, 3)
+    w["fp64_gemv_16384x8192_n"] = lambda: run_gemv_config("f64", 0, 16384, 8192, SEED + 8,
+                                                          steps * 2, 3)
+    w["fp32_syrk_8192x8192"] = lambda: run_syrk_config("f32", 8192, 8192, SEED + 9, steps, 2)
+    w["fp64_syrk_8192x8192"] = lambda: run_syrk_config("f64", 8192, 8192, SEED + 9, steps, 2)
+    return w
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -265,6 +303,15 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.only:
+        import sushiblas_amd as sbx
+        sbx.lib()
+        work = secondary_workloads(args.steps)
+        if args.only not in work:
+            print(f"unknown workload {args.only!r}; one of: {', '.join(work)}", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({"workload": args.only, **work[args.only]()}), flush=True)
         return
     import numpy as np
     import torch
@@ -334,33 +381,10 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.no_also:
-        steps = max(3, min(args.steps, 10))
         also = {}
-        also["fp64_8192_cfg5"] = run_config("f64", 0, 0, 0, 8192, 8192, 8192, 1.0, 0.0,
-                                            SEED + 5, steps, 2)
-        for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
-            also[f"fp32_ragged_cfg3_t{ta}{tb}"] = run_config(
-                "f32", 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3, steps, 2)
-        ts = run_config("f32", 0, 0, 0, 65536, 64, 4096, 1.0, 0.0, SEED + 4, steps, 2,
-                        dist="tall_skinny")
-        ts["hbm_frac"] = round(ts["hbm_gbs"] / HBM_PEAK_GBS, 4)
-        also["fp32_tall_skinny_cfg4"] = ts
-        also["fp32_512_cfg1"] = run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
-                                           steps * 5, 5)
-        also["fp32_gemm_relu_layer_512x1024x1024"] = run_fused_config(512, 1024, 1024, SEED + 6,
-                                                                      steps * 5, 5)
-        also["fp32_gemm_relu_8192x8192x256"] = run_fused_config(8192, 8192, 256, SEED + 7,
-                                                                steps * 2, 3)
-        also["fp32_gemv_16384x16384_n"] = run_gemv_config("f32", 0, 16384, 16384, SEED + 8,
-                                                          steps * 2, 3)
-        also["fp32_gemv_16384x16384_t"] = run_gemv_config("f32", 1, 16384, 16384, SEED + 8,
-                                                          steps * 2, 3)
-        also["fp64_gemv_16384x8192_n"] = run_gemv_config("f64", 0, 16384, 8192, SEED + 8,
-                                                         steps * 2, 3)
-        also["fp32_syrk_8192x8192"] = run_syrk_config("f32", 8192, 8192, SEED + 9, steps, 2)
-        also["fp64_syrk_8192x8192"] = run_syrk_config("f64", 8192, 8192, SEED + 9, steps, 2)
-        for key, entry in also.items():
-            entry["traffic"] = read_traffic(key)
+        for key, fn in secondary_workloads(args.steps).items():
+            also[key] = fn()
+            also[key]["traffic"] = read_traffic(key)
         result["also"] = also
     print(json.dumps(result), flush=True)
     del np

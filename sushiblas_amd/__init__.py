@@ -50,6 +50,14 @@ def lib() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
                            "(or `make -C sushiblas_amd`) first")
+    # torch ships its own HIP runtime.  Loading it first makes libsbx.so bind to
+    # that same runtime (one soname, one instance); loading libsbx.so first
+    # would bring up the system runtime beside torch's, and launches from the
+    # second one to initialise fail with "invalid device function".
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     i64, vp, i32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
     L.sbx_gemm_ex.restype = i32

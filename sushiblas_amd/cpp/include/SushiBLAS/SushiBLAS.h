@@ -4,6 +4,7 @@
 #include <SushiBLAS/core/common.hpp>
 #include <SushiBLAS/core/errors.hpp>
 #include <SushiBLAS/engine.hpp>
+#include <SushiBLAS/io.hpp>
 #include <SushiBLAS/ops/blas.hpp>
 #include <SushiBLAS/ops/math/nonlinear.hpp>
 #include <SushiBLAS/storage.hpp>

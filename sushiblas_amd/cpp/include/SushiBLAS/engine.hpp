@@ -5,6 +5,7 @@
 
 #include <SushiBLAS/core/common.hpp>
 #include <SushiBLAS/core/errors.hpp>
+#include <SushiBLAS/io.hpp>
 #include <SushiBLAS/ops/blas.hpp>
 #include <SushiBLAS/ops/math/nonlinear.hpp>
 #include <SushiBLAS/storage.hpp>
@@ -26,6 +27,8 @@ namespace SushiBLAS
             BLASOps blas() { return BLASOps(*this); }
             /** @brief Activations (engine.hpp:118 of the reference); relu only. */
             NonLinearOps nonlinear() { return NonLinearOps(*this); }
+            /** @brief File IO (engine.hpp:88 of the reference): .npy and raw binary. */
+            IO io() { return IO(*this); }
 
             SushiRuntime::Execution::RuntimeContext& get_context() { return context_; }
             SushiRuntime::Graph::TaskGraph& get_graph() { return graph_; }

@@ -6,13 +6,19 @@
 // tests/runtime/test_dependency_stress.cpp (same fan-out; values checked too).
 // GoogleTest is not available, so a minimal runner stands in: each case is
 // "cpu" (no device needed) or "gpu"; `--cpu`, `--gpu` or case names select.
-// Output: one "[  OK  ] name" or "[FAILED] name: reason" line per case; the
-// exit status is the number of failed cases.
+// Output: one "[  OK  ] name", "[ SKIP ] name: reason" or "[FAILED] name:
+// reason" line per case; the exit status is the number of failed cases.
+// Cases that read fixtures written by numpy take their directory from
+// $SBX_NPY_DIR (tests/test_npy_io.py sets it) and report SKIP without it.
 #include <SushiBLAS/SushiBLAS.h>
+
+#include <unistd.h>
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <functional>
 #include <limits>
 #include <memory>
@@ -25,6 +31,13 @@ namespace
     struct Failure
     {
         std::string what;
+    };
+
+    // A case whose inputs are not available (e.g. a fixture directory that
+    // the Python driver provides) reports SKIP instead of running.
+    struct Skip
+    {
+        std::string why;
     };
 
     struct Case
@@ -810,6 +823,285 @@ TEST_CASE(SyrkBatchedUpperMatchesHostLoop, true)
             }
 }
 
+// -------------------------------------------------------------------- .npy IO
+
+namespace
+{
+    std::string npy_dir()
+    {
+        const char* d = std::getenv("SBX_NPY_DIR");
+        if (!d || !*d) throw Skip{"SBX_NPY_DIR not set"};
+        return d;
+    }
+
+    std::string tmp_path(const std::string& name)
+    {
+        const char* t = std::getenv("TMPDIR");
+        return std::string(t && *t ? t : "/tmp") + "/sbx_io_" + std::to_string(getpid()) + "_" + name;
+    }
+
+    std::string file_bytes(const std::string& path, size_t max_bytes = size_t(-1))
+    {
+        std::ifstream f(path, std::ios::binary);
+        CHECK(f.good());
+        std::string s((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+        return s.substr(0, std::min(max_bytes, s.size()));
+    }
+
+    // host image of a tensor's elements (contiguous tensors)
+    std::vector<char> host_bytes(const sb::Tensor& t)
+    {
+        const size_t n = size_t(t.num_elements) * sb::IO::element_bytes(t.dtype);
+        std::vector<char> out(n);
+        if (t.storage->strategy == AllocStrategy::DEVICE)
+            t.storage->copy_to_host(out.data(), n, t.offset_bytes());
+        else
+            std::memcpy(out.data(), t.data(), n);
+        return out;
+    }
+
+    void set_host_bytes(sb::Tensor& t, const std::vector<char>& in)
+    {
+        if (t.storage->strategy == AllocStrategy::DEVICE)
+            t.storage->copy_from_host(in.data(), in.size(), t.offset_bytes());
+        else
+            std::memcpy(t.data(), in.data(), in.size());
+    }
+} // namespace
+
+TEST_CASE(NpyHeaderEncodeAndParse, false)  // src/io.cpp:136-180
+{
+    const int64_t s23[] = {2, 3};
+    const std::string h = sb::IO::npy_header(DataType::FLOAT32, Layout::ROW_MAJOR, s23, 2);
+    const std::string dict = "{'descr': '<f4', 'fortran_order': False, 'shape': (2, 3), }";
+    CHECK(h.size() == 128);
+    CHECK(h.compare(0, 8, std::string("\x93NUMPY\x01\x00", 8)) == 0);
+    CHECK(static_cast<unsigned char>(h[8]) == 118 && h[9] == 0);  // 128 - 10
+    CHECK(h.compare(10, dict.size(), dict) == 0);
+    CHECK(h.back() == '\n' && h[10 + dict.size()] == ' ');
+    const int64_t s5[] = {5};
+    const std::string h1 = sb::IO::npy_header(DataType::FLOAT64, Layout::COLUMN_MAJOR, s5, 1);
+    CHECK(h1.find("{'descr': '<f8', 'fortran_order': True, 'shape': (5,), }") == 10);
+    CHECK(h1.size() % 64 == 0);
+    for (const std::string& pre : {h, h1})
+    {
+        const sb::NpyHeader p = sb::IO::parse_npy_header(pre);
+        CHECK(p.data_offset == pre.size());
+    }
+    const sb::NpyHeader p = sb::IO::parse_npy_header(h);
+    CHECK(p.descr == "<f4" && !p.fortran_order && p.shape.size() == 2 && p.shape[0] == 2 &&
+          p.shape[1] == 3);
+    const sb::NpyHeader p1 = sb::IO::parse_npy_header(h1);
+    CHECK(p1.descr == "<f8" && p1.fortran_order && p1.shape.size() == 1 && p1.shape[0] == 5);
+    // version 2.0 (4-byte length), other key order and spacing, rank 0
+    std::string d2 = "{\"shape\":(),\"fortran_order\":False,\"descr\":\"<c16\"}\n";
+    std::string v2("\x93NUMPY\x02\x00", 8);
+    for (int i = 0; i < 4; ++i) v2 += static_cast<char>((d2.size() >> (8 * i)) & 0xff);
+    v2 += d2;
+    const sb::NpyHeader q = sb::IO::parse_npy_header(v2);
+    CHECK(q.descr == "<c16" && q.shape.empty() && q.data_offset == v2.size());
+    // malformed
+    CHECK_THROWS(sb::IO::parse_npy_header("\x93NUMPX\x01\x00\x00\x00"));
+    std::string bad = h;
+    bad[10 + dict.find("(2")] = '[';
+    CHECK_THROWS(sb::IO::parse_npy_header(bad));
+    CHECK_THROWS(sb::IO::parse_npy_header(h.substr(0, 40)));  // truncated
+    CHECK(std::string(sb::IO::npy_descr(DataType::HALF)) == "<f2" &&
+          std::string(sb::IO::npy_descr(DataType::COMPLEX32)) == "<c8" &&
+          sb::IO::element_bytes(DataType::COMPLEX64) == 16);
+}
+
+TEST_CASE(NpyHeadersMatchNumpy, false)
+{
+    // headers.txt: "<file> <dtype> <layout> <rank> <d0> <d1> ..." for files np.save wrote
+    const std::string dir = npy_dir();
+    std::ifstream list(dir + "/headers.txt");
+    CHECK(list.good());
+    int n = 0;
+    std::string file;
+    int dtype, layout, rank;
+    while (list >> file >> dtype >> layout >> rank)
+    {
+        int64_t dims[sb::Core::MAX_TENSOR_RANK] = {0};
+        for (int i = 0; i < rank; ++i) list >> dims[i];
+        const std::string want = sb::IO::npy_header(static_cast<DataType>(dtype),
+                                                    static_cast<Layout>(layout), dims, rank);
+        const std::string got = file_bytes(dir + "/" + file, want.size());
+        if (got != want) throw Failure{"header of " + file + " differs from numpy's"};
+        const sb::NpyHeader p = sb::IO::parse_npy_header(file_bytes(dir + "/" + file, 4096));
+        CHECK(static_cast<int>(p.shape.size()) == rank && p.data_offset == want.size());
+        ++n;
+    }
+    CHECK(n > 0);
+}
+
+TEST_CASE(NpyRoundTripEveryStrategyAndType, true)
+{
+    sb::Engine engine(ctx());
+    const DataType types[] = {DataType::FLOAT32, DataType::FLOAT64, DataType::HALF,
+                              DataType::COMPLEX32, DataType::COMPLEX64};
+    const AllocStrategy strats[] = {AllocStrategy::DEVICE, AllocStrategy::SHARED, AllocStrategy::HOST};
+    int which = 0;
+    for (AllocStrategy st : strats)
+        for (DataType dt : types)
+        {
+            // create_tensor(HALF) cannot hold 37 x 53: the Tensor constructor checks
+            // capacity at 4 bytes per element (tensor.hpp:123 of the reference), so
+            // HALF tensors get storage sized that way
+            auto make = [&]() {
+                if (dt != DataType::HALF) return engine.create_tensor({37, 53}, dt, st);
+                auto storage = sr::make_sushi<sb::Storage>(ctx().get_allocator(), 37 * 53 * 4, st);
+                sb::Tensor h(storage, {37, 53});
+                h.dtype = DataType::HALF;
+                return h;
+            };
+            auto t = make();
+            std::vector<char> img(size_t(t.num_elements) * sb::IO::element_bytes(dt));
+            for (size_t i = 0; i < img.size(); ++i) img[i] = char((i * 131 + which * 7) & 0xff);
+            set_host_bytes(t, img);
+            const std::string path = tmp_path("rt" + std::to_string(which++) + ".npy");
+            engine.io().save_npy(t, path);
+            const std::string pre = sb::IO::npy_header(dt, Layout::ROW_MAJOR, t.shape.data(), 2);
+            const std::string bytes = file_bytes(path);
+            CHECK(bytes.size() == pre.size() + img.size());
+            CHECK(bytes.compare(0, pre.size(), pre) == 0);
+            CHECK(std::memcmp(bytes.data() + pre.size(), img.data(), img.size()) == 0);
+            auto u = make();
+            engine.io().load_npy(u, path);
+            CHECK(host_bytes(u) == img);
+            // raw binary dump of the same elements
+            const std::string bin = tmp_path("rt.bin");
+            engine.io().save_bin(t, bin);
+            CHECK(file_bytes(bin) == std::string(img.begin(), img.end()));
+            auto w = make();
+            engine.io().load_bin(w, bin);
+            CHECK(host_bytes(w) == img);
+            std::remove(path.c_str());
+            std::remove(bin.c_str());
+        }
+}
+
+TEST_CASE(NpyViewsOrdersAndErrors, true)
+{
+    // a transposed (non-contiguous) view is written in its logical order
+    sb::Engine engine(ctx());
+    auto X = engine.create_tensor({4, 6}, DataType::FLOAT32, AllocStrategy::DEVICE);
+    std::vector<float> x(24);
+    for (int i = 0; i < 24; ++i) x[i] = float(i) + 0.5f;
+    X.storage->copy_from_host(x.data(), x.size() * 4);
+    auto XT = X.transpose(0, 1);  // 6 x 4 view
+    const std::string p1 = tmp_path("view.npy");
+    engine.io().save_npy(XT, p1);
+    auto Y = engine.create_tensor({6, 4}, DataType::FLOAT32, AllocStrategy::SHARED);
+    engine.io().load_npy(Y, p1);
+    const float* y = Y.data_as<float>();
+    for (int i = 0; i < 6; ++i)
+        for (int j = 0; j < 4; ++j) CHECK(y[i * 4 + j] == x[j * 6 + i]);
+    // reading into a transposed view scatters by strides
+    auto Z = engine.create_tensor({4, 6}, DataType::FLOAT32, AllocStrategy::DEVICE);
+    auto ZT = Z.transpose(0, 1);
+    engine.io().load_npy(ZT, p1);
+    std::vector<float> z(24);
+    Z.storage->copy_to_host(z.data(), 96);
+    CHECK(z == x);
+    // a C-order file read into a column-major tensor is reordered
+    sb::Engine colmajor(ctx(), Layout::COLUMN_MAJOR);
+    auto C = colmajor.create_tensor({6, 4}, DataType::FLOAT32, AllocStrategy::HOST);
+    colmajor.io().load_npy(C, p1);
+    const float* c = C.data_as<float>();
+    for (int i = 0; i < 6; ++i)
+        for (int j = 0; j < 4; ++j) CHECK(c[i + 6 * j] == x[j * 6 + i]);
+    // and written back with fortran_order True, in column-major order
+    const std::string p2 = tmp_path("colmajor.npy");
+    colmajor.io().save_npy(C, p2);
+    const sb::NpyHeader h = sb::IO::parse_npy_header(file_bytes(p2, 4096));
+    CHECK(h.fortran_order && h.shape.size() == 2 && h.shape[0] == 6 && h.shape[1] == 4);
+    // errors: wrong dtype, wrong shape, wrong rank, truncated, bad magic, missing file
+    auto D = engine.create_tensor({6, 4}, DataType::FLOAT64, AllocStrategy::SHARED);
+    CHECK_THROWS(engine.io().load_npy(D, p1));
+    auto E = engine.create_tensor({4, 6}, DataType::FLOAT32, AllocStrategy::SHARED);
+    CHECK_THROWS(engine.io().load_npy(E, p1));
+    auto F = engine.create_tensor({24}, DataType::FLOAT32, AllocStrategy::SHARED);
+    CHECK_THROWS(engine.io().load_npy(F, p1));
+    const std::string full = file_bytes(p1);
+    const std::string p3 = tmp_path("short.npy");
+    {
+        std::ofstream o(p3, std::ios::binary);
+        o << full.substr(0, full.size() - 8);
+    }
+    CHECK_THROWS(engine.io().load_npy(Y, p3));
+    {
+        std::ofstream o(p3, std::ios::binary);
+        o << "NOTNUMPY" << full.substr(8);
+    }
+    CHECK_THROWS(engine.io().load_npy(Y, p3));
+    CHECK_THROWS(engine.io().load_npy(Y, tmp_path("missing.npy")));
+    for (const auto& p : {p1, p2, p3}) std::remove(p.c_str());
+}
+
+TEST_CASE(NpyLargeDeviceTensorStreams, true)
+{
+    // 3 x 100 MB chunks through the pinned double buffer, both directions
+    sb::Engine engine(ctx());
+    const int64_t n = (int64_t(75) << 20) + 17;  // 300 MB + 68 B of fp32
+    auto T = engine.create_tensor({n}, DataType::FLOAT32, AllocStrategy::DEVICE);
+    std::vector<float> v(n);
+    for (int64_t i = 0; i < n; ++i) v[i] = float(i % 1000003) * 0.25f;
+    T.storage->copy_from_host(v.data(), size_t(n) * 4);
+    const std::string p = tmp_path("large.npy");
+    engine.io().save_npy(T, p);
+    auto U = engine.create_tensor({n}, DataType::FLOAT32, AllocStrategy::DEVICE);
+    engine.io().load_npy(U, p);
+    std::vector<float> w(n);
+    U.storage->copy_to_host(w.data(), size_t(n) * 4);
+    CHECK(std::memcmp(w.data(), v.data(), size_t(n) * 4) == 0);
+    std::remove(p.c_str());
+}
+
+TEST_CASE(GoldenGemmThroughNpy, true)
+{
+    // cases.txt: "<name> <dtype> <layout> <ta> <tb> <m> <n> <k> <alpha> <beta>"; the
+    // operands are <name>_{A,B,C,out}.npy written by numpy; the result goes to
+    // <name>_got.npy through save_npy
+    const std::string dir = npy_dir();
+    std::ifstream list(dir + "/cases.txt");
+    CHECK(list.good());
+    std::string name;
+    int dt, layout, ta, tb;
+    int64_t m, n, k;
+    double alpha, beta;
+    int cases = 0;
+    while (list >> name >> dt >> layout >> ta >> tb >> m >> n >> k >> alpha >> beta)
+    {
+        sb::Engine engine(ctx(), static_cast<Layout>(layout));
+        const DataType dtype = static_cast<DataType>(dt);
+        auto A = ta ? engine.create_tensor({k, m}, dtype) : engine.create_tensor({m, k}, dtype);
+        auto B = tb ? engine.create_tensor({n, k}, dtype) : engine.create_tensor({k, n}, dtype);
+        auto C = engine.create_tensor({m, n}, dtype);
+        auto Want = engine.create_tensor({m, n}, dtype);
+        engine.io().load_npy(A, dir + "/" + name + "_A.npy");
+        engine.io().load_npy(B, dir + "/" + name + "_B.npy");
+        engine.io().load_npy(C, dir + "/" + name + "_C.npy");
+        engine.io().load_npy(Want, dir + "/" + name + "_out.npy");
+        engine.blas().gemm(A, B, C, ta != 0, tb != 0, float(alpha), float(beta));
+        engine.io().save_npy(C, dir + "/" + name + "_got.npy");  // runs the GEMM first
+        double num = 0, den = 0;
+        for (int64_t i = 0; i < m * n; ++i)
+        {
+            const double g = dtype == DataType::FLOAT32 ? C.data_as<float>()[i] : C.data_as<double>()[i];
+            const double w = dtype == DataType::FLOAT32 ? Want.data_as<float>()[i]
+                                                        : Want.data_as<double>()[i];
+            num += (g - w) * (g - w);
+            den += w * w;
+        }
+        const double err = den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+        if (err > (dtype == DataType::FLOAT32 ? 1e-5 : 1e-12))
+            throw Failure{name + ": normwise error " + std::to_string(err)};
+        ++cases;
+    }
+    CHECK(cases > 0);
+}
+
 TEST_CASE(LargeFp32MatchesHostLoop, true)
 {
     // 300 x 257 x 129 with odd leading dimensions, against a double host loop
@@ -872,6 +1164,10 @@ int main(int argc, char** argv)
         {
             c.fn();
             std::printf("[  OK  ] %s\n", c.name);
+        }
+        catch (const Skip& k)
+        {
+            std::printf("[ SKIP ] %s: %s\n", c.name, k.why.c_str());
         }
         catch (const Failure& f)
         {

@@ -16,6 +16,9 @@
 //     owns a strip of TC*V consecutive columns; TR = 256/TC thread rows walk
 //     the matrix rows, then reduce through LDS in a fixed order.
 //
+// A is read once, with nontemporal loads (it is not reused, so it should not
+// displace x and the partials from the caches).
+//
 // When rows (resp. column strips) alone cannot fill 256 CUs, the reduction
 // dimension is cut into `chunks` ranges (grid y); each range writes its
 // partial sums to a workspace and gemv_finish_kernel adds them in range order
@@ -74,7 +77,8 @@ __global__ void __launch_bounds__(256) gemv_rows_kernel(GemvArgs<T> p)
                 vec_t av[4], xv[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    av[u] = *reinterpret_cast<const vec_t*>(a + jj + u * LPR * V);
+                    av[u] = __builtin_nontemporal_load(
+                        reinterpret_cast<const vec_t*>(a + jj + u * LPR * V));
                     xv[u] = *reinterpret_cast<const vec_t*>(p.x + jj + u * LPR * V);
                 }
 #pragma unroll
@@ -83,7 +87,7 @@ __global__ void __launch_bounds__(256) gemv_rows_kernel(GemvArgs<T> p)
                     for (int e = 0; e < V; ++e) part[u] += av[u][e] * xv[u][e];
             }
             for (; jj + V <= cv; jj += LPR * V) {
-                const vec_t av = *reinterpret_cast<const vec_t*>(a + jj);
+                const vec_t av = __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(a + jj));
                 const vec_t xv = *reinterpret_cast<const vec_t*>(p.x + jj);
 #pragma unroll
                 for (int e = 0; e < V; ++e) part[0] += av[e] * xv[e];
@@ -91,7 +95,8 @@ __global__ void __launch_bounds__(256) gemv_rows_kernel(GemvArgs<T> p)
             acc = (part[0] + part[1]) + (part[2] + part[3]);
             j = cv;
         }
-        for (int64_t jj = j + gl; jj < c1; jj += LPR) acc += a[jj] * p.x[jj * p.incx];
+        for (int64_t jj = j + gl; jj < c1; jj += LPR)
+            acc += __builtin_nontemporal_load(a + jj) * p.x[jj * p.incx];
     }
     // reduce over the LPR lanes of the group (fixed butterfly order)
 #pragma unroll
@@ -131,7 +136,8 @@ __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
                 T xs[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    av[u] = *reinterpret_cast<const vec_t*>(p.A + (i + u * TR) * p.lda + col);
+                    av[u] = __builtin_nontemporal_load(
+                        reinterpret_cast<const vec_t*>(p.A + (i + u * TR) * p.lda + col));
                     xs[u] = p.x[(i + u * TR) * p.incx];
                 }
 #pragma unroll
@@ -140,7 +146,8 @@ __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
                     for (int e = 0; e < VC; ++e) acc[e] += av[u][e] * xs[u];
             }
             for (; i < r1; i += TR) {
-                const vec_t av = *reinterpret_cast<const vec_t*>(p.A + i * p.lda + col);
+                const vec_t av =
+                    __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(p.A + i * p.lda + col));
                 const T xs = p.x[i * p.incx];
 #pragma unroll
                 for (int e = 0; e < VC; ++e) acc[e] += av[e] * xs;
@@ -150,7 +157,8 @@ __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
                 const T xs = p.x[i * p.incx];
 #pragma unroll
                 for (int e = 0; e < VC; ++e)
-                    if (col + e < p.cols) acc[e] += p.A[i * p.lda + col + e] * xs;
+                    if (col + e < p.cols)
+                        acc[e] += __builtin_nontemporal_load(p.A + i * p.lda + col + e) * xs;
             }
         }
     }
@@ -187,8 +195,17 @@ __global__ void __launch_bounds__(256) gemv_finish_kernel(GemvArgs<T> p, int64_t
 {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= len) return;
-    T s = p.ws[e];
-    for (int c = 1; c < chunks; ++c) s += p.ws[(int64_t)c * len + e];
+    // loads issued 8 at a time so they overlap; the additions keep chunk order
+    T s = 0;
+    int c = 0;
+    for (; c + 8 <= chunks; c += 8) {
+        T v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = p.ws[(int64_t)(c + q) * len + e];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s = (c + q == 0) ? v[q] : s + v[q];
+    }
+    for (; c < chunks; ++c) s = (c == 0) ? p.ws[e] : s + p.ws[(int64_t)c * len + e];
     T* yp = p.y + e * p.incy;
     *yp = finish(s, p.alpha, p.beta, yp);
 }
@@ -216,7 +233,11 @@ template <typename T>
 GemvPlan plan_gemv(bool trans, int64_t rows, int64_t cols, bool vec, int cus)
 {
     constexpr int V = 16 / (int)sizeof(T);
-    const int64_t target = (int64_t)cus * 8;  // workgroups that keep HBM busy
+    // Workgroups wanted before the reduction dimension is cut.  Both forms
+    // stream best with few long-lived workgroups (measured, fp32: transposed
+    // 16384^2 at 6.3 TB/s with 256 workgroups and 4.8 TB/s with 4096; 256 x
+    // 1M untransposed at 6.8 TB/s with 512 and 6.2 TB/s with 2048).
+    const int64_t target = trans ? (int64_t)cus : (int64_t)cus * 2;
     GemvPlan pl{};
     pl.trans = trans;
     pl.vec = vec;
