@@ -14,9 +14,12 @@
  *     memory (or pinned host memory mapped into the device address space).
  *     The library never frees or retains a caller pointer.
  *   - Launches are asynchronous on `stream` (NULL = the null stream of the
- *     current device).  The only allocation is the split-K workspace for
- *     under-filled grids: cached per (device, stream), grown with hipMalloc
- *     the first time a larger one is needed, reused after that.
+ *     current device).  The only allocation is the workspace for split-K
+ *     GEMM/SYRK partials and chunked GEMV partials: cached per (device,
+ *     stream), grown with hipMalloc (at least doubling) the first time a
+ *     larger one is needed and reused after that; an outgrown buffer is kept,
+ *     not freed, until the process ends.  If the allocation fails the call
+ *     runs without splitting instead of failing.
  *   - Return value is a status code (sbx_status); nothing throws across the
  *     ABI.  The C++ layer turns codes into std::runtime_error, as the
  *     reference's SB_THROW_IF does (include/SushiBLAS/core/logger.hpp:316-323).
@@ -25,8 +28,10 @@
  *     propagate).
  *   - layout 0 = row-major, 1 = column-major (Core::Layout,
  *     include/SushiBLAS/core/common.hpp:41-45).  transA/transB: 0 or 1.
- *   - Re-entrant: no mutable global state; safe to call from any host thread
+ *   - Re-entrant: the only global state is the per-device CU count and the
+ *     workspace cache, both behind mutexes; safe to call from any host thread
  *     (the reference runs the GEMM closure on a scheduler worker thread).
+ *     Calls on one stream share its workspace and run in stream order.
  */
 #ifndef SBX_H
 #define SBX_H

@@ -140,7 +140,7 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 // fixed order (deterministic).  The partials live in a workspace cached per
 // (device, stream): calls on one stream are ordered, so they can share it; the
 // first call that needs more memory grows it (the only allocation on the GEMM
-// path, once per stream and size).
+// path; outgrown buffers are kept, see stream_workspace).
 // ---------------------------------------------------------------------------
 constexpr int kMaxSplit = kMaxSplitParts;
 
@@ -195,7 +195,11 @@ std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace>* g_ws =
     new std::map<std::pair<int, hipStream_t>, Workspace>();
 
-// A workspace of at least `bytes` for `stream`, or nullptr.
+// A workspace of at least `bytes` for `stream`, or nullptr.  A workspace that
+// is outgrown is retired, not freed: another host thread may hold its address
+// for a launch it has not enqueued yet, so freeing it (even after a stream
+// synchronize) could race with that launch.  Growth at least doubles, so the
+// retired buffers add up to less than the live one.
 void* stream_workspace(hipStream_t stream, size_t bytes)
 {
     int dev = 0;
@@ -203,17 +207,11 @@ void* stream_workspace(hipStream_t stream, size_t bytes)
     std::lock_guard<std::mutex> g(g_ws_mutex);
     Workspace& w = (*g_ws)[{dev, stream}];
     if (w.bytes < bytes) {
-        if (w.base) {
-            if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
-            (void)hipFree(w.base);
-            w.base = nullptr;
-            w.bytes = 0;
-        }
         size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
-        if (hipMalloc(&w.base, nb) != hipSuccess) {
-            w.base = nullptr;
-            return nullptr;
-        }
+        if (nb < 2 * w.bytes) nb = 2 * w.bytes;
+        void* p = nullptr;
+        if (hipMalloc(&p, nb) != hipSuccess) return nullptr;  // the old one stays usable
+        w.base = p;
         w.bytes = nb;
     }
     return w.base;

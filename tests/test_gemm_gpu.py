@@ -329,6 +329,49 @@ def test_split_k_is_deterministic(cuda, dtype):
     assert normwise(0, g1, want, m, n, ldc) <= TOL[dtype]
 
 
+def test_workspace_growth_under_concurrent_host_threads(cuda):
+    """Host threads share one (fresh) stream and mix a small split-K shape
+    (workspace within the initial size) with a 256x256-tile shape whose split
+    tail needs a larger workspace, so the cache grows while other threads may
+    hold the old address.  Every result must match the oracle."""
+    import threading
+    import torch
+    import sushiblas_amd as sbx
+    shapes = [(512, 512, 512), (4608, 4096, 512)]
+    assert "splitk8" in sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4096, 512, 512, 4096, 4096)
+    data = []
+    for i, (m, n, k) in enumerate(shapes):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)
+        want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+        data.append((m, n, k, torch.from_numpy(A).to(cuda), lda, torch.from_numpy(B).to(cuda),
+                     ldb, ldc, want))
+    stream = torch.cuda.Stream()
+    outs = [[torch.zeros(d[0] * d[1], device=cuda) for _ in range(3)] for d in data]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        try:
+            for rep in range(3):
+                for j in ((t + rep) % 2, (t + rep + 1) % 2):
+                    m, n, k, dA, lda, dB, ldb, ldc, _ = data[j]
+                    sbx.sgemm(0, 0, 0, m, n, k, 1.0, dA, lda, dB, ldb, 0.0, outs[j][t % 3], ldc,
+                              stream=stream)
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(6)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    stream.synchronize()
+    assert not errors, errors
+    for (m, n, k, _, _, _, _, ldc, want), group in zip(data, outs):
+        for o in group:
+            assert normwise(0, o.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32]
+
+
 def test_split_k_on_two_streams(cuda):
     """Each stream has its own split-K workspace: concurrent calls on two
     streams do not corrupt each other."""
