@@ -193,27 +193,51 @@ struct GemmArgs {
     int tiles;  // tiles in the grid: tiles_m * tiles_n, or T(T+1)/2 for a triangle
 };
 
-// Tile id -> (tile row, tile column).  Whole C: GROUP_M-tall column walk, so
-// consecutive ids share B column panels and a group's A row panels.  Triangle:
-// row-by-row over the lower triangle (row r holds tiles 0..r), mirrored for
-// upper, so consecutive ids share the A row panel.
+// Tile id -> (tile row, tile column).
+//  Whole C: GROUP_M-tall column walk, so consecutive ids share B column panels
+//  and a group's A row panels.
+//  Triangle (lower; upper is its mirror): the tile rows form bands of GROUP_M;
+//  band [r0, r1) holds ids [r0(r0+1)/2, r1(r1+1)/2) and walks its columns in
+//  order, top to bottom -- first the full-height columns left of the band's
+//  diagonal block, then the triangular columns inside it -- the same panel
+//  sharing as the GROUP_M walk, restricted to the triangle.
+__device__ inline int64_t tri_count(int r) { return (int64_t)r * (r + 1) / 2; }
+
 template <typename T>
 __device__ inline void tile_coords(const GemmArgs<T>& p, int id, int& tm, int& tn)
 {
+    const int G = p.group_m;
     if (p.uplo == 0) {
-        const int group_span = p.group_m * p.tiles_n;
+        const int group_span = G * p.tiles_n;
         const int group = id / group_span;
-        const int first_m = group * p.group_m;
-        const int gsize = min(p.tiles_m - first_m, p.group_m);
+        const int first_m = group * G;
+        const int gsize = min(p.tiles_m - first_m, G);
         const int in_group = id - group * group_span;
         tm = first_m + in_group % gsize;
         tn = in_group / gsize;
         return;
     }
-    int r = (int)((sqrtf(8.0f * (float)id + 1.0f) - 1.0f) * 0.5f);
-    while (r > 0 && r * (r + 1) / 2 > id) --r;
-    while ((r + 1) * (r + 2) / 2 <= id) ++r;
-    const int c = id - r * (r + 1) / 2;
+    // band of id: the plain row-by-row row index, rounded down to the band
+    int r0 = (int)((sqrtf(8.0f * (float)id + 1.0f) - 1.0f) * 0.5f);
+    r0 -= r0 % G;
+    while (r0 > 0 && tri_count(r0) > id) r0 -= G;
+    while (tri_count(min(r0 + G, p.tiles_m)) <= id) r0 += G;
+    const int h = min(r0 + G, p.tiles_m) - r0;
+    int rest = id - (int)tri_count(r0);
+    int r, c;
+    if (rest < r0 * h) {
+        c = rest / h;
+        r = r0 + rest % h;
+    } else {
+        rest -= r0 * h;
+        int j = 0;  // column r0 + j of the diagonal block holds h - j tiles
+        while (rest >= h - j) {
+            rest -= h - j;
+            ++j;
+        }
+        c = r0 + j;
+        r = r0 + j + rest;
+    }
     if (p.uplo == 1) { tm = r; tn = c; }
     else { tm = c; tn = r; }
 }
