@@ -71,23 +71,39 @@ const CfgInfo kCfg[] = {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-Cfg choose_cfg(int dtype, int64_t m, int64_t n, int uplo = 0)
+// Tile configurations worth modelling for a problem, the default first.
+int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
 {
     if (uplo) {
         // a triangle needs square tiles, so diagonal tiles are the tm == tn ones
-        if (dtype != SBX_F32) return F64_128x128;
+        if (dtype != SBX_F32) {
+            out[0] = F64_128x128;
+            return 1;
+        }
         const int64_t t = cdiv(n, 256);
-        return t * (t + 1) / 2 >= 256 ? F32_256x256 : F32_128x128;
+        out[0] = t * (t + 1) / 2 >= 256 ? F32_256x256 : F32_128x128;
+        return 1;
     }
-    if (dtype == SBX_F32) {
-        if (n <= 64) return F32_128x64;
-        if (m <= 64) return F32_64x128;
-        if (cdiv(m, 256) * cdiv(n, 256) >= 256) return F32_256x256;
-        return F32_128x128;
+    const bool f32 = dtype == SBX_F32;
+    const Cfg sq = f32 ? F32_128x128 : F64_128x128;
+    const Cfg tall = f32 ? F32_128x64 : F64_128x64;   // n <= 64 (tall-skinny)
+    const Cfg wide = f32 ? F32_64x128 : F64_64x128;   // m <= 64
+    if (n <= 64) {
+        out[0] = tall;
+        return 1;
     }
-    if (n <= 64) return F64_128x64;
-    if (m <= 64) return F64_64x128;
-    return F64_128x128;
+    if (m <= 64) {
+        out[0] = wide;
+        return 1;
+    }
+    if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 256) {
+        out[0] = F32_256x256;  // full rounds of the largest tile
+        return 1;
+    }
+    out[0] = sq;
+    out[1] = m >= n ? tall : wide;
+    out[2] = m >= n ? wide : tall;
+    return 3;
 }
 
 // Row-major operand facts for the MFMA kernels.
@@ -133,14 +149,29 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 }
 
 // ---------------------------------------------------------------------------
-// Split-K of under-filled grids.  With S resident slots (CUs x workgroups per
-// CU), a grid of T tiles runs ceil(T/S) rounds; when the last round would be
-// less than 60 % full (or T < S), those tail tiles are cut into `split`
-// k-ranges so the last round is full, and a second kernel sums the parts in
-// fixed order (deterministic).  The partials live in a workspace cached per
-// (device, stream): calls on one stream are ordered, so they can share it; the
-// first call that needs more memory grows it (the only allocation on the GEMM
-// path; outgrown buffers are kept, see stream_workspace).
+// Kernel choice and split-K from a cost model fitted to measurements of these
+// kernels on MI355X (fp32; 512^3 .. 3000^3, the ragged 4095x3001x2047, K from
+// 300 to 4096; predictions within about 10 %, and the ranking right in
+// interleaved A/B runs):
+//   * a workgroup's work is w = 2*BM*BN*K_part / R, R = 0.55 TFLOP/s per CU
+//     (fp32; 0.275 fp64);
+//   * a config keeps P workgroups per CU (its waves per SIMD); a round of
+//     P*CUs workgroups takes P*w; a partial round whose busiest CU holds
+//     q < P workgroups takes q*w/e1, where e1 is what a CU achieves without
+//     its co-resident partner (0.95 with 16-byte loads, 0.85 when an operand
+//     needs scalar loads);
+//   * the grid adds F = 8 us once (pipeline fill and the last epilogue; in
+//     between, co-resident workgroups hide each other's);
+//   * a split adds the reduction kernel, G + (partial bytes it reads) / W with
+//     G = 2.5 us and W = 6 TB/s (the partial writes overlap the GEMM).
+// Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
+// may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
+// faster, another tile shape if >= 3 % faster than the default.
+// Split partials live in a workspace cached per (device, stream): calls on
+// one stream are ordered, so they can share it; the first call that needs
+// more memory grows it (the only allocation on the GEMM path; outgrown
+// buffers are kept, see stream_workspace).  The reduction sums the parts in
+// fixed order, so results are deterministic.
 // ---------------------------------------------------------------------------
 constexpr int kMaxSplit = kMaxSplitParts;
 
@@ -150,22 +181,62 @@ struct SplitPlan {
     int rem;
 };
 
-SplitPlan plan_split(int64_t tiles, int64_t slots, int64_t nk, int64_t batch)
+struct Choice {
+    Cfg cfg;
+    SplitPlan sp;
+    double seconds;  // model prediction
+};
+
+int64_t tile_count(const Problem& p, Cfg c)
 {
-    SplitPlan none{(int)tiles, 1, 0};
-    if (batch > 1 || nk < 4) return none;
-    int64_t rem, split;
-    if (tiles >= slots) {
-        rem = tiles % slots;
-        if (rem == 0 || rem * 10 >= slots * 6) return none;
-    } else {
-        rem = tiles;
+    const CfgInfo& ci = kCfg[c];
+    if (p.uplo) {
+        const int64_t t = cdiv(p.n, ci.bn);
+        return t * (t + 1) / 2;
     }
-    split = slots / rem;
-    if (split > kMaxSplit) split = kMaxSplit;
-    if (split > nk / 2) split = nk / 2;
-    if (split < 2) return none;
-    return SplitPlan{(int)(tiles - rem), (int)split, (int)rem};
+    return cdiv(p.m, ci.bm) * cdiv(p.n, ci.bn);
+}
+
+// Modelled time of `units` workgroups of `work` seconds each.
+double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, double e1)
+{
+    if (units <= 0) return 0.0;
+    const int64_t slots = per_cu * cus;
+    double t = (double)(units / slots) * (double)per_cu * work;
+    const int64_t left = units % slots;
+    if (left) {
+        const int64_t q = cdiv(left, cus);
+        t += (double)q * work / (q == per_cu ? 1.0 : e1);
+    }
+    return t;
+}
+
+Choice model_plan(const Problem& p, Cfg c, int64_t cus, bool vector_loads)
+{
+    const CfgInfo& ci = kCfg[c];
+    const double rate = p.dtype == SBX_F32 ? 0.55e12 : 0.275e12;
+    const double F = 8e-6, G = 2.5e-6, W = 6e12;
+    const double e1 = vector_loads ? 0.95 : 0.85;
+    const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
+    const double w = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // one whole tile
+    const int64_t P = ci.per_cu;
+    const int64_t tiles = tile_count(p, c);
+    const int64_t units = tiles * (p.batch > 1 ? p.batch : 1);
+    Choice best{c, SplitPlan{(int)tiles, 1, 0}, rounds_time(units, w, P, cus, e1) + F};
+    const int64_t nk = cdiv(p.k, ci.bk);
+    if (p.batch > 1 || nk < 4) return best;
+    const int64_t rem = tiles >= P * cus ? tiles % (P * cus) : tiles;
+    if (rem == 0) return best;
+    const int64_t full = tiles - rem;
+    const int64_t smax = nk / 2 < kMaxSplit ? nk / 2 : kMaxSplit;
+    for (int64_t sp = 2; sp <= smax; ++sp) {
+        const double t = rounds_time(full, w, P, cus, e1) +
+                         rounds_time(rem * sp, w / (double)sp, P, cus, e1) + F + G +
+                         (double)(rem * sp) * ci.bm * ci.bn * elem / W;
+        if (t < best.seconds * 0.98)
+            best = Choice{c, SplitPlan{(int)full, (int)sp, (int)rem}, t};
+    }
+    return best;
 }
 
 std::mutex g_cu_mutex;
@@ -259,18 +330,32 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
-    Cfg cfg = choose_cfg(p.dtype, p.m, p.n, p.uplo);
-    if (algo == SBX_ALGO_GENERIC) cfg = GENERIC;
-    if (cfg != GENERIC && !mfma_feasible(p, cfg)) {
-        if (algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
-        cfg = GENERIC;
+    Cfg cfg = GENERIC;
+    SplitPlan sp{0, 1, 0};
+    if (algo != SBX_ALGO_GENERIC) {
+        Cfg cands[3];
+        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cands);
+        const int64_t cus = cu_count();
+        bool any = false;
+        Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
+        const size_t el = p.dtype == SBX_F32 ? 4 : 8;
+        const bool vec = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch, p.A, el).vec &&
+                         plan_operand(p.tb, p.tb ? p.k : p.n, p.ldb, p.str_b, p.batch, p.B, el).vec;
+        for (int i = 0; i < nc; ++i) {
+            if (!mfma_feasible(p, cands[i])) continue;
+            const Choice c = model_plan(p, cands[i], cus, vec);
+            if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
+            any = true;
+        }
+        if (!any && algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
+        if (any) {
+            cfg = best.cfg;
+            sp = best.sp;
+        }
     }
     const CfgInfo& info = kCfg[cfg];
-    const int64_t tiles = p.uplo ? cdiv(p.n, info.bn) * (cdiv(p.n, info.bn) + 1) / 2
-                                 : cdiv(p.m, info.bm) * cdiv(p.n, info.bn);
-    SplitPlan sp{(int)tiles, 1, 0};
-    if (cfg != GENERIC && !quick)
-        sp = plan_split(tiles, (int64_t)cu_count() * info.per_cu, cdiv(p.k, info.bk), p.batch);
+    const int64_t tiles = tile_count(p, cfg);
+    if (cfg == GENERIC || quick) sp = SplitPlan{(int)tiles, 1, 0};
     if (chosen) *chosen = cfg;
     if (chosen_split) *chosen_split = sp;
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only

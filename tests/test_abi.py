@@ -85,7 +85,7 @@ def test_noop_cases_need_no_device():
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w2x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2+splitk2"),
-    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_128x128x16_w2x2+splitk8"),
+    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_128x64x32_w2x2+splitk8"),
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
     (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x128x32_w2x2+splitk5"),
     (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
@@ -101,10 +101,27 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     assert sbx.gemm_select(dtype, layout, ta, tb, m, n, k, lda, ldb, ldc) == expect
 
 
+@pytest.mark.parametrize("m,n,k,expect", [
+    (1024, 1024, 1024, "mfma_f32_128x64x32_w2x2+splitk2"),     # under one round of 128x128
+    (512, 1024, 1024, "mfma_f32_64x128x32_w2x2+splitk4"),
+    (2048, 2048, 2048, "mfma_f32_128x64x32_w2x2"),             # one full round of 512 slots
+    (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
+    (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
+])
+def test_model_based_selection(m, n, k, expect):
+    """Tile shape and split from the cost model (whole rounds unsplit, the
+    tail cut only when the model predicts a gain).  Each choice was timed on
+    the device against the alternatives."""
+    assert sbx.gemm_select(0, 0, 0, 0, m, n, k, k, n, n) == expect
+
+
 def test_huge_leading_dimension_falls_back_to_generic():
     """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
-    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
+    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \
         "generic_64x64x16"
+    # 2^22: 128-row tiles overflow, 64-row tiles still fit -> an MFMA kernel
+    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024).startswith(
+        "mfma_f32_64x128")
 
 
 def test_fused_gemm_validation():

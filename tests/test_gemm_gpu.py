@@ -338,7 +338,9 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
     import torch
     import sushiblas_amd as sbx
     shapes = [(512, 512, 512), (4608, 4096, 512)]
-    assert "splitk8" in sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4096, 512, 512, 4096, 4096)
+    # 32 tail tiles of 256x256 cut into >= 5 parts: > 32 MB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4096, 512, 512, 4096, 4096)
+    assert name.startswith("mfma_f32_256x256") and int(name.split("splitk")[1]) >= 5, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)
