@@ -16,7 +16,9 @@ Printed as one JSON line.  Besides the contract fields it carries:
   also          -- the other BASELINE configs timed the same way (fp64 8192^3,
                    the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), the
                    fused GEMM+ReLU epilogue against GEMM followed by ReLU, GEMV
-                   (HBM GB/s) and SYRK (TFLOP/s over the triangle)
+                   (HBM GB/s), SYRK (TFLOP/s over the triangle), and the C++
+                   Engine/TaskGraph path on the reference's framework-sim
+                   patterns (microseconds per batch, one lane vs four)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
                        [--cpu-seconds S] [--no-cpu]
@@ -282,6 +284,25 @@ def run_syrk_config(dtype, n, k, seed, steps, warmup):
     return out
 
 
+def engine_patterns():
+    """The C++ Engine path (Level3::gemm / NonLinearOps::relu recorded into the
+    TaskGraph, then Engine::execute()) on the reference's integration patterns,
+    timed by sushiblas_amd/lib/sushiblas_engine_bench: one lane vs all lanes."""
+    import subprocess
+    exe = os.path.join(ROOT, "sushiblas_amd", "lib", "sushiblas_engine_bench")
+    res = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                         timeout=300)
+    if res.returncode != 0:
+        raise RuntimeError("sushiblas_engine_bench failed:\n" + res.stdout[-2000:])
+    out = {}
+    for line in res.stdout.splitlines():
+        if line.startswith("{"):
+            r = json.loads(line)
+            e = out.setdefault(r["pattern"], {"tasks": r["tasks"]})
+            e[f"us_per_batch_lanes{r['lanes']}"] = r["us_per_batch"]
+    return out
+
+
 def secondary_workloads(steps_arg):
     """The `also` workloads in run order, as key -> thunk."""
     steps = max(3, min(steps_arg, 10))
@@ -312,6 +333,7 @@ def secondary_workloads(steps_arg):
                                                           steps * 2, 3)
     w["fp32_syrk_8192x8192"] = lambda: run_syrk_config("f32", 8192, 8192, SEED + 9, steps, 2)
     w["fp64_syrk_8192x8192"] = lambda: run_syrk_config("f64", 8192, 8192, SEED + 9, steps, 2)
+    w["engine_task_graph"] = engine_patterns
     return w
 
 
@@ -404,7 +426,8 @@ def main():
         also = {}
         for key, fn in secondary_workloads(args.steps).items():
             also[key] = fn()
-            also[key]["traffic"] = read_traffic(key)
+            if key != "engine_task_graph":
+                also[key]["traffic"] = read_traffic(key)
         result["also"] = also
     print(json.dumps(result), flush=True)
     del np

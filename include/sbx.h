@@ -31,7 +31,9 @@
  *   - Re-entrant: the only global state is the per-device CU count and the
  *     workspace cache, both behind mutexes; safe to call from any host thread
  *     (the reference runs the GEMM closure on a scheduler worker thread).
- *     Calls on one stream share its workspace and run in stream order.
+ *     Calls on one stream share its workspace and run in stream order; the
+ *     two kernels of a split call are enqueued under that stream's lock, so
+ *     concurrent host threads on one stream cannot interleave with them.
  */
 #ifndef SBX_H
 #define SBX_H
@@ -109,6 +111,20 @@ int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, 
                    int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
                    int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
                    void* C, int64_t ldc, int64_t str_c, int64_t batch, int epilogue);
+
+/* Grouped GEMM: `count` problems C_i = epilogue(alpha*op(A_i)*op(B_i) +
+ * beta*C_i) with one shape, one set of leading dimensions and scalars, and
+ * operands anywhere in device memory: `table` is a DEVICE array of 3*count
+ * pointers (A_0, B_0, C_0, A_1, B_1, C_1, ...), read by the kernel in stream
+ * order.  aligned16 != 0 promises every pointer is 16-byte aligned (enables
+ * 16-byte loads).  One launch for all of them.  No single counterpart in the
+ * reference: it is how the task graph issues a run of independent,
+ * same-shaped Level3::gemm tasks (each one gemm.cpp:63 / :76 call in the
+ * reference, run on worker threads) without one launch per task. */
+int sbx_gemm_grouped(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                     int64_t n, int64_t k, const void* alpha, int64_t lda, int64_t ldb,
+                     const void* beta, int64_t ldc, const void* const* table, int64_t count,
+                     int aligned16, int epilogue);
 
 /* x[i] = x[i] > 0 ? x[i] : 0 for n contiguous elements of dtype: the
  * stand-alone ReLU (replaces the body of NonLinearOps::relu,

@@ -13,11 +13,13 @@
 // sycl::event becomes Execution::Event (a HIP event; a default-constructed
 // Event is already complete, like a default sycl::event).
 //
-// Scheduling: the reference's TaskGraph resolves read/write dependencies
-// by base pointer and runs tasks on worker threads.  Here every task of a
-// graph is issued, in record order, onto the context's single in-order HIP
-// stream, which already orders every RAW/WAR/WAW pair; execute() returns an
-// Event for the whole batch.
+// Scheduling: the reference's TaskGraph resolves read/write dependencies by
+// base pointer and runs independent tasks in parallel on worker threads.  Here
+// the same dependencies (RAW, WAW, WAR over the access sets' base pointers)
+// place each task on one of a few HIP streams ("lanes") of the context:
+// dependent tasks follow their latest dependency's lane or wait on an event
+// recorded on the other lane, independent ones spread round-robin; execute()
+// joins the lanes and returns an Event for the whole batch.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -172,7 +174,7 @@ namespace SushiRuntime
 
     namespace Execution
     {
-        /** @brief Owns the HIP device, its stream and allocator
+        /** @brief Owns the HIP device, its streams and allocator
          *  (execution/runtime_context.hpp:42-96).  The device is touched on
          *  first use (std::call_once), so a context -- and an Engine over it --
          *  can be built, and GEMM arguments validated, on a host without a GPU. */
@@ -189,14 +191,21 @@ namespace SushiRuntime
                 Queue& get_queue(size_t xpu_index = 0);
                 sushi_ptr<Memory::USMAllocator> get_allocator();
                 int device() const { return device_; }
+                /** @brief Wait for every lane of the device. */
                 void wait_all();
+
+                /** @brief Streams the task graph spreads independent tasks over
+                 *  (stands in for the reference's worker threads,
+                 *  task_scheduler.hpp:79).  Lane 0 is get_queue(0). */
+                static constexpr size_t kLanes = 4;
+                Queue& get_lane(size_t lane);
 
             private:
                 void init();
                 int device_ = 0;
                 std::once_flag once_;
-                hipStream_t stream_ = nullptr;
-                std::unique_ptr<Queue> queue_;
+                hipStream_t streams_[kLanes] = {};
+                std::unique_ptr<Queue> lanes_[kLanes];
                 sushi_ptr<Memory::USMAllocator> allocator_;
         };
     } // namespace Execution
@@ -286,11 +295,52 @@ namespace SushiRuntime
             const char* fused_name = nullptr;  // PRODUCER: task name once fused
         };
 
+        /** @brief Grouping description of a task: consecutive independent
+         *  tasks with equal `key`s (same launch parameters) are issued as one
+         *  launch over a device table of their operand pointers. */
+        struct GroupHook
+        {
+            bool enabled = false;
+            uint64_t key[8] = {};
+            const void* ptrs[3] = {};  // this task's A, B, C device addresses
+            bool aligned = false;      // all three 16-byte aligned
+            int epilogue = 0;          // 1 once a ReLU has been fused into the task
+            /** Issue `count` problems whose pointers are at `table` (device). */
+            std::function<void(Execution::Queue&, const void* const* table, int64_t count,
+                               bool aligned, int epilogue)>
+                launch;
+        };
+
+        /** @brief A task as the grouping planner sees it. */
+        struct GroupCandidate
+        {
+            const GroupHook* group = nullptr;  // null or !enabled: not groupable
+            bool has_deps = false;             // explicit event dependencies
+            const std::vector<void*>* reads = nullptr;
+            const std::vector<void*>* writes = nullptr;
+        };
+
+        /** @brief One run of tasks issued as a single grouped launch. */
+        struct GroupRun
+        {
+            size_t first = 0;        // index of the first task
+            size_t count = 0;        // tasks (>= 2)
+            int64_t table_offset = 0;  // first problem in the table (3 pointers each)
+            bool aligned = true;     // every pointer 16-byte aligned
+        };
+
+        /** @brief Runs of consecutive groupable tasks with equal keys and
+         *  epilogues and no hazard among them, and the pointer table (A, B, C
+         *  per task, in task order) that their launches read. */
+        std::vector<GroupRun> plan_groups(const std::vector<GroupCandidate>& tasks,
+                                          std::vector<const void*>& table);
+
         /** @brief Record-then-execute task list (graph/task_graph.hpp:55-124). */
         class TaskGraph
         {
             public:
                 explicit TaskGraph(Execution::RuntimeContext& ctx) : ctx_(ctx) {}
+                ~TaskGraph();
                 TaskGraph(const TaskGraph&) = delete;
                 TaskGraph& operator=(const TaskGraph&) = delete;
 
@@ -308,8 +358,22 @@ namespace SushiRuntime
                               FusionHook fusion,
                               const std::vector<Execution::Event>& dependencies = {});
 
-                /** @brief Issue every recorded task in order; returns an Event that
-                 *  completes when all of them (and the staging copies) have.  A
+                /** @brief As above, with fusion and grouping descriptions. */
+                void add_task(const TaskMetadata& meta, const std::vector<void*>& read_access,
+                              const std::vector<void*>& write_access, HostWork work,
+                              FusionHook fusion, GroupHook group,
+                              const std::vector<Execution::Event>& dependencies = {});
+
+                /** @brief Issue every recorded task; returns an Event that completes
+                 *  when all of them (and the staging copies) have.
+                 *  Dependencies come from the access sets, as in the reference
+                 *  (task_graph.hpp:107-117): a task waits for the last writer of
+                 *  everything it reads or writes and for every reader of what it
+                 *  writes since that write (RAW, WAW, WAR).  Independent tasks are
+                 *  spread over the context's lanes (HIP streams); a task runs on
+                 *  the lane of its latest dependency, so chains stay in one
+                 *  stream, and a dependency on another lane becomes an event
+                 *  wait.  Trace hooks see the tasks in record order.  A
                  *  PRODUCER task directly followed by a RELU task over the same
                  *  region (same base, offset, element count and type, no extra
                  *  dependencies) is issued once, as its fused form. */
@@ -319,6 +383,11 @@ namespace SushiRuntime
                 void set_trace_hook(TraceHook hook);
                 /** @brief Turn GEMM+ReLU fusion on (default) or off. */
                 void set_fusion(bool enabled);
+                /** @brief Use at most `lanes` streams (1 = strictly in order). */
+                void set_max_lanes(size_t lanes);
+                /** @brief Turn grouped launches of same-shaped independent tasks
+                 *  on (default) or off. */
+                void set_grouping(bool enabled);
 
             private:
                 struct Task
@@ -328,12 +397,29 @@ namespace SushiRuntime
                     HostWork work;
                     std::vector<Execution::Event> deps;
                     FusionHook fusion;
+                    GroupHook group;
+                    // a grouped task: the members' metadata (for the trace hook)
+                    // and its slice of the batch's pointer table
+                    std::vector<TaskMetadata> members;
+                    int64_t table_offset = -1;  // first problem (3 pointers each)
+                    int64_t table_count = 0;    // problems
+                    bool table_aligned = false;
                 };
                 Execution::RuntimeContext& ctx_;
                 mutable std::mutex mu_;
                 std::vector<Task> tasks_;
                 TraceHook trace_;
                 bool fusion_ = true;
+                size_t max_lanes_ = Execution::RuntimeContext::kLanes;
+                size_t next_lane_ = 0;
+                hipEvent_t lane_events_[Execution::RuntimeContext::kLanes] = {};
+                bool grouping_ = true;
+                // pointer tables of grouped tasks: pinned staging -> device,
+                // one copy per batch on lane 0
+                void* table_dev_ = nullptr;
+                void* table_pin_ = nullptr;
+                size_t table_cap_ = 0;  // pointers
+                hipEvent_t table_copied_ = nullptr;
         };
     } // namespace Graph
 } // namespace SushiRuntime

@@ -8,11 +8,15 @@
 // stream where the reference's gemm_dispatch<T> (gemm.cpp:44-79) calls oneMKL.
 // The task also carries a fusion description (its output run and a ReLU-fused
 // form of the same work), which TaskGraph::execute() uses when a ReLU over
-// exactly that run is recorded next.
+// exactly that run is recorded next, and a grouping description (launch
+// parameters, operand addresses and a grouped launcher) that lets execute()
+// issue a run of independent same-shaped GEMMs as one launch.
 #include <SushiBLAS/engine.hpp>
 #include <SushiBLAS/ops/blas/level3.hpp>
 
 #include "../../../include/sbx.h"
+
+#include <cstring>
 
 namespace SushiBLAS
 {
@@ -90,6 +94,43 @@ namespace SushiBLAS
             fusion.fused_name = "blas.lvl3.gemm+relu";
         }
 
+        // Unbatched FLOAT32/FLOAT64 GEMMs may be issued together with other
+        // tasks of equal launch parameters (one grouped launch over a table of
+        // operand pointers); the key holds every parameter but the pointers.
+        SushiRuntime::Graph::GroupHook group;
+        if (batch_size == 1 && (A.dtype == Core::DataType::FLOAT32 || A.dtype == Core::DataType::FLOAT64) &&
+            A.storage && B.storage && C.storage && m > 0 && n > 0)
+        {
+            const int dt = A.dtype == Core::DataType::FLOAT32 ? SBX_F32 : SBX_F64;
+            uint32_t ab, bb;
+            std::memcpy(&ab, &alpha, 4);
+            std::memcpy(&bb, &beta, 4);
+            group.enabled = true;
+            group.key[0] = uint64_t(dt) | uint64_t(layout) << 8 | uint64_t(tA) << 9 | uint64_t(tB) << 10;
+            group.key[1] = uint64_t(m);
+            group.key[2] = uint64_t(n);
+            group.key[3] = uint64_t(k);
+            group.key[4] = uint64_t(lda);
+            group.key[5] = uint64_t(ldb);
+            group.key[6] = uint64_t(ldc);
+            group.key[7] = uint64_t(ab) << 32 | bb;
+            group.ptrs[0] = A.device_data();
+            group.ptrs[1] = B.device_data();
+            group.ptrs[2] = C.device_data();
+            group.aligned = true;
+            for (const void* ptr : group.ptrs) group.aligned = group.aligned && (uintptr_t)ptr % 16 == 0;
+            group.launch = [=](Queue& q, const void* const* table, int64_t count, bool aligned,
+                               int epilogue) {
+                const double ad = alpha, bd = beta;
+                const void* pa = dt == SBX_F32 ? static_cast<const void*>(&alpha) : &ad;
+                const void* pb = dt == SBX_F32 ? static_cast<const void*>(&beta) : &bd;
+                const int st = sbx_gemm_grouped(q.native(), dt, layout, tA, tB, m, n, k, pa, lda, ldb,
+                                                pb, ldc, table, count, aligned ? 1 : 0, epilogue);
+                SB_THROW_IF(st != SBX_OK, "grouped GEMM [{}x{}x{}, {} problems] failed: {}", m, n, k,
+                            count, sbx_status_string(st));
+            };
+        }
+
         auto& graph = engine_.get_graph();
         switch (A.dtype)
         {
@@ -110,7 +151,8 @@ namespace SushiBLAS
                 };
                 if (fusion.kind != SushiRuntime::Graph::FusionHook::NONE)
                     fusion.with_relu = work(SBX_EPILOGUE_RELU);
-                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion));
+                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion),
+                               group);
                 break;
             }
             case Core::DataType::FLOAT64:
@@ -132,7 +174,8 @@ namespace SushiBLAS
                 };
                 if (fusion.kind != SushiRuntime::Graph::FusionHook::NONE)
                     fusion.with_relu = work(SBX_EPILOGUE_RELU);
-                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion));
+                graph.add_task(meta, reads, writes, work(SBX_EPILOGUE_NONE), std::move(fusion),
+                               group);
                 break;
             }
             case Core::DataType::HALF:

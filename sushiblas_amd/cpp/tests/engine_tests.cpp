@@ -430,12 +430,17 @@ TEST_CASE(FrameworkSimParallelBatchedInference, true)  // test_framework_sim.cpp
         weights.push_back(W);
         outputs.push_back(engine.create_tensor({m, n}));
     }
+    std::vector<std::string> names;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
     for (int i = 0; i < num_models; ++i)
     {
         engine.blas().gemm(inputs[i], weights[i], outputs[i]);
         engine.nonlinear().relu(outputs[i]);
     }
     engine.execute().wait();
+    // every GEMM+ReLU pair fused; the 24 fused tasks go out as one grouped launch
+    CHECK(names.size() == size_t(num_models));
+    for (const auto& nm : names) CHECK(nm == "blas.lvl3.gemm+relu");
     for (int i = 0; i < num_models; ++i)
     {
         CHECK(outputs[i].shape[0] == m && outputs[i].shape[1] == n);
@@ -719,6 +724,73 @@ TEST_CASE(GemvSyrkValidationThrowsAtRecordTime, false)
     Sh.dtype = Ch.dtype = DataType::HALF;
     CHECK_THROWS(e.blas().syrk(Sh, Ch));
     CHECK(e.get_graph().pending() == 0);
+}
+
+TEST_CASE(GroupPlannerRunsAndTableOffsets, false)
+{
+    // host-only: runs break at key/epilogue changes, explicit deps and hazards;
+    // every run's table slice holds exactly its members' pointers, in order
+    struct Fake
+    {
+        sr::Graph::GroupHook g;
+        std::vector<void*> r, w;
+        bool deps = false;
+    };
+    std::vector<Fake> f(12);
+    char mem[64][16];
+    auto P = [&](int i) { return static_cast<void*>(mem[i]); };
+    for (int i = 0; i < 12; ++i)
+    {
+        f[i].g.enabled = true;
+        f[i].g.key[1] = 8;
+        f[i].g.ptrs[0] = P(3 * i);
+        f[i].g.ptrs[1] = P(3 * i + 1);
+        f[i].g.ptrs[2] = P(3 * i + 2);
+        f[i].g.aligned = (i % 5) != 4;
+        f[i].g.launch = [](sr::Execution::Queue&, const void* const*, int64_t, bool, int) {};
+        f[i].r = {P(3 * i), P(3 * i + 1)};
+        f[i].w = {P(3 * i + 2)};
+    }
+    f[3].g.key[1] = 9;                 // breaks the run 0..2
+    f[6].g.epilogue = 1;               // breaks 4..5
+    f[8].r[0] = f[7].w[0];             // RAW on 7: breaks 6? no: 6 has another epilogue; 7..8 broken
+    f[10].deps = true;                 // not groupable
+    std::vector<sr::Graph::GroupCandidate> c(12);
+    for (int i = 0; i < 12; ++i) c[i] = sr::Graph::GroupCandidate{&f[i].g, f[i].deps, &f[i].r, &f[i].w};
+    std::vector<const void*> table;
+    const auto runs = sr::Graph::plan_groups(c, table);
+    // expected runs: [0,3), [4,6), [8,10) (8 starts a new run after the hazard), none after
+    CHECK(runs.size() == 3);
+    const size_t firsts[] = {0, 4, 8}, counts[] = {3, 2, 2};
+    int64_t off = 0;
+    for (size_t k = 0; k < runs.size(); ++k)
+    {
+        CHECK(runs[k].first == firsts[k] && runs[k].count == counts[k]);
+        CHECK(runs[k].table_offset == off);
+        bool aligned = true;
+        for (size_t q = 0; q < runs[k].count; ++q)
+        {
+            const auto& g = f[runs[k].first + q].g;
+            for (int e = 0; e < 3; ++e) CHECK(table[3 * (runs[k].table_offset + q) + e] == g.ptrs[e]);
+            aligned = aligned && g.aligned;
+        }
+        CHECK(runs[k].aligned == aligned);
+        off += static_cast<int64_t>(runs[k].count);
+    }
+    CHECK(table.size() == size_t(3 * off));
+    // a WAR inside a run: task 1 writes what task 0 reads
+    std::vector<Fake> h(2);
+    for (int i = 0; i < 2; ++i)
+    {
+        h[i].g = f[0].g;
+        h[i].w = {P(40 + i)};
+    }
+    h[0].r = {P(50)};
+    h[1].r = {P(51)};
+    h[1].w = {P(50)};
+    std::vector<sr::Graph::GroupCandidate> c2 = {{&h[0].g, false, &h[0].r, &h[0].w},
+                                                 {&h[1].g, false, &h[1].r, &h[1].w}};
+    CHECK(sr::Graph::plan_groups(c2, table).empty() && table.empty());
 }
 
 TEST_CASE(SimpleGEMV, true)  // tests/blas/level2/test_gemv.cpp
@@ -1100,6 +1172,150 @@ TEST_CASE(GoldenGemmThroughNpy, true)
         ++cases;
     }
     CHECK(cases > 0);
+}
+
+// ------------------------------------------------------------ multi-lane DAG
+
+namespace
+{
+    // Runs a seeded random DAG of GEMMs over `nbuf` shared 192x192 buffers
+    // (dst = 0.01 * src1 * src2 + 0.5 * dst, with RAW/WAR/WAW hazards all
+    // over) on `lanes` lanes; returns every buffer's bytes afterwards.
+    std::vector<float> random_dag(size_t lanes, int nbuf, int nops, unsigned seed, bool grouping = true)
+    {
+        sb::Engine engine(ctx());
+        engine.get_graph().set_max_lanes(lanes);
+        engine.get_graph().set_grouping(grouping);
+        const int n = 192;
+        std::vector<sb::Tensor> bufs;
+        unsigned x = seed;
+        auto next = [&] { x = x * 1664525u + 1013904223u; return x >> 8; };
+        for (int b = 0; b < nbuf; ++b)
+        {
+            bufs.push_back(engine.create_tensor({n, n}));
+            std::vector<float> v(n * n);
+            for (auto& e : v) e = float(int(next() % 2001) - 1000) / 1000.0f;
+            fill_tensor(bufs.back(), v);
+        }
+        for (int i = 0; i < nops; ++i)
+        {
+            const int s1 = int(next() % nbuf), s2 = int(next() % nbuf);
+            int d = int(next() % nbuf);
+            while (d == s1 || d == s2) d = (d + 1) % nbuf;
+            engine.blas().gemm(bufs[s1], bufs[s2], bufs[d], next() % 2 == 0, false, 0.01f, 0.5f);
+        }
+        engine.execute().wait();
+        std::vector<float> out;
+        for (auto& b : bufs) out.insert(out.end(), b.data_as<float>(), b.data_as<float>() + n * n);
+        return out;
+    }
+} // namespace
+
+TEST_CASE(RandomDagSameBitsOnOneOrFourLanes, true)
+{
+    // the in-order single lane is the reference schedule: every hazard the
+    // multi-lane schedule misses shows up as different bits
+    for (unsigned seed : {1u, 7u, 2026u})
+    {
+        const auto one = random_dag(1, 6, 60, seed);
+        const auto four = random_dag(4, 6, 60, seed);
+        CHECK(one.size() == four.size());
+        CHECK(std::memcmp(one.data(), four.data(), one.size() * sizeof(float)) == 0);
+    }
+}
+
+TEST_CASE(GroupedLaunchesMatchSingleLaunches, true)
+{
+    // grouping changes only how launches are formed (one batched launch may
+    // pick another tile or split than a single one): same values to rounding
+    for (unsigned seed : {3u, 11u})
+    {
+        const auto grouped = random_dag(4, 8, 80, seed, true);
+        const auto single = random_dag(1, 8, 80, seed, false);
+        double num = 0, den = 0;
+        for (size_t i = 0; i < single.size(); ++i)
+        {
+            num += double(grouped[i] - single[i]) * (grouped[i] - single[i]);
+            den += double(single[i]) * single[i];
+        }
+        CHECK(std::sqrt(num / den) <= 1e-5);
+    }
+}
+
+TEST_CASE(GroupedRunsTraceEveryTaskAndStopAtHazards, true)
+{
+    sb::Engine engine(ctx());
+    std::vector<std::string> names;
+    engine.get_graph().set_trace_hook([&](const sr::Graph::TaskMetadata& m) { names.push_back(m.name); });
+    const int N = 16, ops = 40;
+    std::vector<sb::Tensor> A, C;
+    auto B = engine.create_tensor({N, N});
+    fill_tensor(B, std::vector<float>(N * N, 1.0f));
+    for (int i = 0; i < ops; ++i)
+    {
+        A.push_back(engine.create_tensor({N, N}));
+        C.push_back(engine.create_tensor({N, N}));
+        fill_tensor(A.back(), std::vector<float>(N * N, float(i + 1)));
+    }
+    // 40 independent GEMMs (one grouped launch), then a GEMM that reads C[0]
+    // (RAW on the run: must come after it), then 40 more reading C[i] into A[i]
+    for (int i = 0; i < ops; ++i) engine.blas().gemm(A[i], B, C[i]);
+    auto D = engine.create_tensor({N, N});
+    engine.blas().gemm(C[0], B, D);
+    for (int i = 0; i < ops; ++i) engine.blas().gemm(C[i], B, A[i], false, false, 0.5f, 0.0f);
+    engine.execute().wait();
+    CHECK(names.size() == size_t(2 * ops + 1));
+    for (const auto& nm : names) CHECK(nm == "blas.lvl3.gemm");
+    for (int i = 0; i < ops; ++i)
+    {
+        verify_tensor(C[i], std::vector<float>(N * N, float(N * (i + 1))), 0.0);
+        verify_tensor(A[i], std::vector<float>(N * N, 0.5f * N * N * (i + 1)), 0.0);
+    }
+    verify_tensor(D, std::vector<float>(N * N, float(N * N)), 0.0);
+}
+
+TEST_CASE(CrossLaneRawAndWar, true)
+{
+    sb::Engine engine(ctx());
+    std::vector<std::string> names;
+    const int n = 1024;
+    auto X = engine.create_tensor({n, n});
+    auto W = engine.create_tensor({n, n});
+    auto C0 = engine.create_tensor({n, n});
+    auto U = engine.create_tensor({64, 64});
+    auto V = engine.create_tensor({64, 64});
+    auto D = engine.create_tensor({64, 64});
+    std::vector<float> x(n * n), w(n * n);
+    for (int i = 0; i < n * n; ++i)
+    {
+        x[i] = float((i * 7) % 13) - 6.0f;
+        w[i] = float((i * 5) % 11) - 5.0f;
+    }
+    fill_tensor(X, x);
+    fill_tensor(W, w);
+    fill_tensor(U, std::vector<float>(64 * 64, 1.0f));
+    fill_tensor(V, std::vector<float>(64 * 64, 2.0f));
+    // T0 reads X (slow, 1024^3); T1 is independent (another lane); T2 reads
+    // T1's D and overwrites X's first 64x64 block: it must wait for T0 on the
+    // other lane (WAR) and for T1 (RAW)
+    engine.blas().gemm(X, W, C0);
+    engine.blas().gemm(U, V, D);
+    sb::Tensor X64(X.storage, {64, 64});  // first 64*64 elements of X's storage
+    engine.blas().gemm(D, V, X64);
+    engine.execute().wait();
+    // C0 from the original X, exact (small integers)
+    const float* c0 = C0.data_as<float>();
+    for (int i = 0; i < n; i += 97)
+        for (int j = 0; j < n; j += 89)
+        {
+            double sacc = 0;
+            for (int k = 0; k < n; ++k) sacc += double(x[i * n + k]) * w[k * n + j];
+            CHECK(c0[i * n + j] == float(sacc));
+        }
+    // D = 1*2*64 = 128 everywhere, X64 = D*V = 128*2*64
+    verify_tensor(D, std::vector<float>(64 * 64, 128.0f), 0.0);
+    const float* xb = X.data_as<float>();
+    for (int i = 0; i < 64 * 64; ++i) CHECK(xb[i] == 16384.0f);
 }
 
 TEST_CASE(LargeFp32MatchesHostLoop, true)

@@ -28,10 +28,10 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs<T> p)
     // a triangle (SYRK) skips the tiles wholly outside it
     if ((p.uplo == 1 && tn > tm) || (p.uplo == 2 && tn < tm)) return;
     const int64_t m0 = (int64_t)tm * 64, n0 = (int64_t)tn * 64;
-    const int64_t bz = blockIdx.z;
-    const T* A = p.A + bz * p.str_a;
-    const T* B = p.B + bz * p.str_b;
-    T* C = p.C + bz * p.str_c;
+    const T* A;
+    const T* B;
+    T* C;
+    batch_bases(p, (int64_t)blockIdx.z, A, B, C);
 
     T acc[4][4];
 #pragma unroll
@@ -115,9 +115,11 @@ template hipError_t launch_generic<double>(const GemmArgs<double>&, bool, bool, 
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t str_c, int64_t m,
-                                                    int64_t n, T beta, int relu, int uplo)
+                                                    int64_t n, T beta, int relu, int uplo,
+                                                    const void* const* table)
 {
-    T* c = C + (int64_t)blockIdx.z * str_c;
+    T* c = table ? static_cast<T*>(const_cast<void*>(table[3 * (int64_t)blockIdx.z + 2]))
+                 : C + (int64_t)blockIdx.z * str_c;
     const int64_t total = m * n;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * 256) {
@@ -131,20 +133,21 @@ __global__ void __launch_bounds__(256) scale_kernel(T* C, int64_t ldc, int64_t s
 
 template <typename T>
 hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
-                        int relu, int uplo, int batch, hipStream_t stream)
+                        int relu, int uplo, int batch, hipStream_t stream,
+                        const void* const* table)
 {
     int64_t blocks = (m * n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     if (blocks < 1) blocks = 1;
     scale_kernel<T><<<dim3((unsigned)blocks, 1, (unsigned)batch), dim3(256), 0, stream>>>(
-        C, ldc, str_c, m, n, beta, relu, uplo);
+        C, ldc, str_c, m, n, beta, relu, uplo, table);
     return hipGetLastError();
 }
 
 template hipError_t launch_scale<float>(float*, int64_t, int64_t, int64_t, int64_t, float, int,
-                                        int, int, hipStream_t);
+                                        int, int, hipStream_t, const void* const*);
 template hipError_t launch_scale<double>(double*, int64_t, int64_t, int64_t, int64_t, double,
-                                         int, int, int, hipStream_t);
+                                         int, int, int, hipStream_t, const void* const*);
 
 // ---------------------------------------------------------------------------
 // Elementwise ReLU over n contiguous elements (the stand-alone form of the

@@ -191,7 +191,29 @@ struct GemmArgs {
     // tiles_n = T and only the T(T+1)/2 tiles that meet the triangle exist.
     int uplo;
     int tiles;  // tiles in the grid: tiles_m * tiles_n, or T(T+1)/2 for a triangle
+    // Grouped launch: batch entry z takes its operands from a device table of
+    // 3 pointers per entry (A, B, C as the caller names them; with
+    // table_swap the first two trade places, for the column-major mapping)
+    // instead of base + z * stride.  Null: strided.
+    const void* const* table;
+    int table_swap;
 };
+
+// Operand and result bases of batch entry z.
+template <typename T>
+__device__ inline void batch_bases(const GemmArgs<T>& p, int64_t z, const T*& A, const T*& B, T*& C)
+{
+    if (p.table) {
+        const void* const* e = p.table + 3 * z;
+        A = static_cast<const T*>(e[p.table_swap ? 1 : 0]);
+        B = static_cast<const T*>(e[p.table_swap ? 0 : 1]);
+        C = static_cast<T*>(const_cast<void*>(e[2]));
+    } else {
+        A = p.A + z * p.str_a;
+        B = p.B + z * p.str_b;
+        C = p.C + z * p.str_c;
+    }
+}
 
 // Tile id -> (tile row, tile column).
 //  Whole C: GROUP_M-tall column walk, so consecutive ids share B column panels
@@ -451,10 +473,10 @@ gemm_mfma_kernel(GemmArgs<T> p)
     tile_coords(p, id, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int64_t bz = blockIdx.z;
-    const T* A = p.A + bz * p.str_a;
-    const T* B = p.B + bz * p.str_b;
-    T* C = p.C + bz * p.str_c;
+    const T* A;
+    const T* B;
+    T* C;
+    batch_bases(p, (int64_t)blockIdx.z, A, B, C);
 
     // ---- operand tile bases and extents ----
     // A k-contiguous: element (m, k) at m*lda + k; x-contiguous: at k*lda + m.
@@ -711,7 +733,11 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
 #pragma unroll
     for (int q = 1; q < kMaxSplitParts; ++q)
         if (q < p.split) sum += v[q];
-    T* cp = p.C + (int64_t)blockIdx.z * p.str_c + (int64_t)m * p.ldc + n;
+    const T* Az;
+    const T* Bz;
+    T* Cz;
+    batch_bases(p, (int64_t)blockIdx.z, Az, Bz, Cz);
+    T* cp = Cz + (int64_t)m * p.ldc + n;
     T out = p.alpha * sum;
     if (p.beta != (T)0) out += p.beta * *cp;
     *cp = p.relu ? relu_of(out) : out;

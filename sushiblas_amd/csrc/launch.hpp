@@ -21,10 +21,12 @@ hipError_t launch_generic(const GemmArgs<T>& a, bool trans_a, bool trans_b, int 
                           hipStream_t stream);
 
 // C <- beta*C (beta == 0 stores zeros without reading C), then ReLU if relu;
-// uplo 1 / 2: only the lower / upper triangle.
+// uplo 1 / 2: only the lower / upper triangle; with a grouped-launch table,
+// entry z's C is table[3z + 2].
 template <typename T>
 hipError_t launch_scale(T* C, int64_t ldc, int64_t str_c, int64_t m, int64_t n, T beta,
-                        int relu, int uplo, int batch, hipStream_t stream);
+                        int relu, int uplo, int batch, hipStream_t stream,
+                        const void* const* table = nullptr);
 
 // x <- max(x, 0) elementwise (NaN -> 0) over n contiguous elements.
 template <typename T>

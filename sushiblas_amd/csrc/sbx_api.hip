@@ -42,6 +42,11 @@ struct Problem {
     int64_t batch;
     int relu;  // fused ReLU epilogue
     int uplo;  // 0: whole C; 1 / 2: lower / upper triangle only (SYRK, B == A, m == n)
+    // grouped launch: batch entry z's A, B, C come from this device table
+    // (3 pointers per entry); A/B/C above are then 16-byte aligned (or not)
+    // stand-in addresses that only carry the alignment facts
+    const void* const* table;
+    int table_swap;
 };
 
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
@@ -260,32 +265,49 @@ int cu_count()
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
+    // Held from handing out the workspace until the calls that use it are
+    // enqueued: a split GEMM (or chunked GEMV) is two kernels, and another
+    // host thread's call on the same stream must not land between them and
+    // overwrite the partials the second kernel is about to read.
+    std::mutex launch_mu;
 };
 std::mutex g_ws_mutex;
 // never destroyed: freeing device memory during process teardown is unsafe
 std::map<std::pair<int, hipStream_t>, Workspace>* g_ws =
     new std::map<std::pair<int, hipStream_t>, Workspace>();
 
-// A workspace of at least `bytes` for `stream`, or nullptr.  A workspace that
-// is outgrown is retired, not freed: another host thread may hold its address
-// for a launch it has not enqueued yet, so freeing it (even after a stream
-// synchronize) could race with that launch.  Growth at least doubles, so the
-// retired buffers add up to less than the live one.
-void* stream_workspace(hipStream_t stream, size_t bytes)
+// A stream's workspace with its launch lock held.
+struct WorkspaceLease {
+    void* ptr = nullptr;
+    std::unique_lock<std::mutex> lock;
+};
+
+// A workspace of at least `bytes` for `stream` (ptr null if it cannot be
+// allocated), locked for the caller's launches.  A workspace that is outgrown
+// is retired, not freed: kernels enqueued earlier on the stream may not have
+// run yet.  Growth at least doubles, so the retired buffers add up to less
+// than the live one.
+WorkspaceLease stream_workspace(hipStream_t stream, size_t bytes)
 {
+    WorkspaceLease lease;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> g(g_ws_mutex);
-    Workspace& w = (*g_ws)[{dev, stream}];
-    if (w.bytes < bytes) {
-        size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
-        if (nb < 2 * w.bytes) nb = 2 * w.bytes;
-        void* p = nullptr;
-        if (hipMalloc(&p, nb) != hipSuccess) return nullptr;  // the old one stays usable
-        w.base = p;
-        w.bytes = nb;
+    if (hipGetDevice(&dev) != hipSuccess) return lease;
+    Workspace* w;
+    {
+        std::lock_guard<std::mutex> g(g_ws_mutex);
+        w = &(*g_ws)[{dev, stream}];  // map nodes never move
     }
-    return w.base;
+    lease.lock = std::unique_lock<std::mutex>(w->launch_mu);
+    if (w->bytes < bytes) {
+        size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
+        if (nb < 2 * w->bytes) nb = 2 * w->bytes;
+        void* p = nullptr;
+        if (hipMalloc(&p, nb) != hipSuccess) return lease;  // ptr null; the old one stays
+        w->base = p;
+        w->bytes = nb;
+    }
+    lease.ptr = w->base;
+    return lease;
 }
 
 hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan pb,
@@ -360,9 +382,10 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (chosen_split) *chosen_split = sp;
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
     void* ws = nullptr;
+    WorkspaceLease lease;  // held until both split kernels are enqueued
     if (sp.split > 1) {
-        ws = stream_workspace(stream, (size_t)sp.rem * sp.split * info.bm *
-                                                         info.bn * sizeof(T));
+        lease = stream_workspace(stream, (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T));
+        ws = lease.ptr;
         if (!ws) sp = SplitPlan{(int)tiles, 1, 0};  // no memory: run unsplit
     }
 
@@ -371,7 +394,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         hipError_t e;
         if (quick) {
             e = launch_scale<T>((T*)p.C + b0 * p.str_c, p.ldc, p.str_c, p.m, p.n, beta, p.relu,
-                                p.uplo, nb, stream);
+                                p.uplo, nb, stream, p.table ? p.table + 3 * b0 : nullptr);
         } else {
             GemmArgs<T> a;
             a.A = (const T*)p.A + b0 * p.str_a;
@@ -393,6 +416,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.relu = p.relu;
             a.uplo = p.uplo;
             a.tiles = (int)tiles;
+            a.table = p.table ? p.table + 3 * b0 : nullptr;
+            a.table_swap = p.table_swap;
             const size_t elem = sizeof(T);
             const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
                                                 a.A, elem);
@@ -450,6 +475,8 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     p.k = k; p.C = C; p.ldc = ldc; p.str_c = batch > 1 ? str_c : 0; p.batch = batch;
     p.relu = epilogue == SBX_EPILOGUE_RELU;
     p.uplo = 0;
+    p.table = nullptr;
+    p.table_swap = 0;
     if (batch <= 1) { p.str_a = 0; p.str_b = 0; }
 
     hipStream_t s = (hipStream_t)stream;
@@ -458,6 +485,54 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
                           chosen_split);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
                        chosen_split);
+}
+
+// Grouped GEMM: `count` problems of one shape and one set of scalars whose
+// operands are scattered (a device table of A_i, B_i, C_i pointers), run as
+// one batched launch -- what the task graph uses to issue runs of
+// independent same-shaped GEMMs without one launch each.
+int grouped_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                 int64_t n, int64_t k, const void* alpha, int64_t lda, int64_t ldb,
+                 const void* beta, int64_t ldc, const void* const* table, int64_t count,
+                 int aligned16, int epilogue)
+{
+    if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
+    if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
+    if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return SBX_INVALID_ARGUMENT;
+    if (m < 0 || n < 0 || k < 0 || count < 0) return SBX_INVALID_ARGUMENT;
+    if (m > kMaxDim || n > kMaxDim || k > kMaxDim) return SBX_UNSUPPORTED;
+    if (!alpha || !beta) return SBX_INVALID_ARGUMENT;
+    if (check_ld(layout, transA, m, k, lda) || check_ld(layout, transB, k, n, ldb) ||
+        check_ld(layout, false, m, n, ldc))
+        return SBX_INVALID_ARGUMENT;
+    if (m == 0 || n == 0 || count == 0) return SBX_OK;
+    if (!table || (uintptr_t)table % sizeof(void*)) return SBX_INVALID_ARGUMENT;
+    // alignment stand-ins: never dereferenced, they carry the caller's promise
+    const void* stand_in = (const void*)(uintptr_t)(aligned16 ? 0x1000 : 0x1004);
+    Problem p;
+    p.dtype = dtype;
+    if (layout == 0) {
+        p.ta = transA; p.tb = transB; p.m = m; p.n = n;
+        p.lda = lda; p.ldb = ldb;
+        p.table_swap = 0;
+    } else {
+        p.ta = transB; p.tb = transA; p.m = n; p.n = m;
+        p.lda = ldb; p.ldb = lda;
+        p.table_swap = 1;
+    }
+    p.A = stand_in; p.B = stand_in; p.C = const_cast<void*>(stand_in);
+    p.str_a = 0; p.str_b = 0; p.str_c = 0;
+    p.k = k; p.ldc = ldc; p.batch = count;
+    p.relu = epilogue == SBX_EPILOGUE_RELU;
+    p.uplo = 0;
+    p.table = table;
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SBX_F32)
+        return run<float>(p, *(const float*)alpha, *(const float*)beta, SBX_ALGO_AUTO, s, nullptr,
+                          nullptr);
+    return run<double>(p, *(const double*)alpha, *(const double*)beta, SBX_ALGO_AUTO, s, nullptr,
+                       nullptr);
 }
 
 // SYRK: C = alpha * op(A) op(A)^T + beta * C on one triangle of the n x n C
@@ -500,6 +575,8 @@ int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t
     p.batch = batch;
     p.relu = 0;
     p.uplo = up ? 2 : 1;
+    p.table = nullptr;
+    p.table_swap = 0;
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, SBX_ALGO_AUTO, s,
@@ -534,8 +611,10 @@ int gemv_run(hipStream_t stream, bool trans, int64_t rows, int64_t cols, T alpha
     a.alpha = alpha; a.beta = beta;
     a.cw = pl.cw;
     a.ws = nullptr;
+    WorkspaceLease lease;  // held until the partial and finish kernels are enqueued
     if (pl.chunks > 1) {
-        a.ws = (T*)stream_workspace(stream, (size_t)pl.chunks * pl.out_len * sizeof(T));
+        lease = stream_workspace(stream, (size_t)pl.chunks * pl.out_len * sizeof(T));
+        a.ws = (T*)lease.ptr;
         if (!a.ws) {  // no memory for partials: one range
             pl.chunks = 1;
             pl.cw = trans ? rows : cols;
@@ -598,6 +677,16 @@ int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, 
     return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
                           B, ldb, str_b, beta, C, ldc, str_c, batch, SBX_ALGO_AUTO, epilogue,
                           nullptr, nullptr);
+}
+
+int sbx_gemm_grouped(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                     int64_t n, int64_t k, const void* alpha, int64_t lda, int64_t ldb,
+                     const void* beta, int64_t ldc, const void* const* table, int64_t count,
+                     int aligned16, int epilogue)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    return sbx::grouped_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, lda, ldb,
+                             beta, ldc, table, count, aligned16, epilogue);
 }
 
 int sbx_relu(void* stream, int dtype, void* x, int64_t n)

@@ -189,3 +189,28 @@ def test_syrk_validation():
     assert syrk(batch=2, sc=0) == 1
     assert syrk(n=0) == 0 and syrk(batch=0) == 0
     assert syrk(n=1 << 31) == 2
+
+
+def test_grouped_gemm_validation():
+    """sbx_gemm_grouped: host-side checks; empty work needs no device."""
+    L = sbx.lib()
+    one = ctypes.c_float(1.0)
+    vp = ctypes.c_void_p
+
+    def grouped(count=2, table=4096, epilogue=0, lda=4, m=4, dtype=0):
+        L.sbx_gemm_grouped.restype = ctypes.c_int
+        L.sbx_gemm_grouped.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp,
+                                       ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_int64, vp,
+                                       ctypes.c_int64, ctypes.c_int, ctypes.c_int]
+        return L.sbx_gemm_grouped(0, dtype, 0, 0, 0, m, 4, 4, ctypes.byref(one), lda, 4,
+                                  ctypes.byref(one), 4, table, count, 1, epilogue)
+
+    assert grouped(epilogue=3) == 1
+    assert grouped(lda=3) == 1
+    assert grouped(count=-1) == 1
+    assert grouped(table=0) == 1           # no table for a non-empty group
+    assert grouped(table=4097) == 1        # misaligned table
+    assert grouped(dtype=5) == 2
+    assert grouped(count=0, table=0) == 0  # nothing to do
+    assert grouped(m=0) == 0
