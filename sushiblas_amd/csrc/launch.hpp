@@ -38,6 +38,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 #define SBX_MFMA_CONFIGS(X)  \
     X(float, 256, 256, 32, 2, 2, 1, 1) \
     X(float, 128, 128, 16, 2, 2, 2, 2) \
+    X(float, 128, 128, 16, 2, 2, 2, 3) \
     X(float, 128, 64, 32, 2, 2, 2, 2) \
     X(float, 64, 128, 32, 2, 2, 2, 2) \
     X(double, 128, 128, 16, 2, 2, 1, 2) \

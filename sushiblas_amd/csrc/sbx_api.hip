@@ -53,6 +53,7 @@ struct Problem {
 enum Cfg {
     F32_256x256,   // large fp32: 4 waves of 128x128, 1 wave/SIMD (256 accumulators)
     F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
+    F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
     F32_64x128,    // m <= 64
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
@@ -69,6 +70,7 @@ struct CfgInfo {
 
 const CfgInfo kCfg[] = {
     {"mfma_f32_256x256x32_w2x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
+    {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"generic_64x64x16", 64, 64, 16, 4},
@@ -105,10 +107,12 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         out[0] = F32_256x256;  // full rounds of the largest tile
         return 1;
     }
-    out[0] = sq;
-    out[1] = m >= n ? tall : wide;
-    out[2] = m >= n ? wide : tall;
-    return 3;
+    int c = 0;
+    out[c++] = sq;
+    if (f32) out[c++] = F32_128x128_O3;
+    out[c++] = m >= n ? tall : wide;
+    out[c++] = m >= n ? wide : tall;
+    return c;
 }
 
 // Row-major operand facts for the MFMA kernels.
@@ -155,20 +159,22 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 
 // ---------------------------------------------------------------------------
 // Kernel choice and split-K from a cost model fitted to measurements of these
-// kernels on MI355X (fp32; 512^3 .. 3000^3, the ragged 4095x3001x2047, K from
-// 300 to 4096; predictions within about 10 %, and the ranking right in
-// interleaved A/B runs):
+// kernels on MI355X: every candidate tile x split of 24 fp32 and 24 fp64
+// shapes (512^3 .. 4096^3, the ragged 4095x3001x2047 in all four transposes,
+// K from 300 to 8192); the model's pick is on average within 0.7 % of the
+// fastest measured candidate, and at most 7 % off:
 //   * a workgroup's work is w = 2*BM*BN*K_part / R, R = 0.55 TFLOP/s per CU
 //     (fp32; 0.275 fp64);
 //   * a config keeps P workgroups per CU (its waves per SIMD); a round of
 //     P*CUs workgroups takes P*w; a partial round whose busiest CU holds
-//     q < P workgroups takes q*w/e1, where e1 is what a CU achieves without
-//     its co-resident partner (0.95 with 16-byte loads, 0.85 when an operand
+//     q < P workgroups takes q*w/e1, where e1 is what a CU achieves short of
+//     its co-resident partners (0.9 with 16-byte loads, 0.85 when an operand
 //     needs scalar loads);
-//   * the grid adds F = 8 us once (pipeline fill and the last epilogue; in
+//   * the grid adds F = 4 us once (pipeline fill and the last epilogue; in
 //     between, co-resident workgroups hide each other's);
-//   * a split adds the reduction kernel, G + (partial bytes it reads) / W with
-//     G = 2.5 us and W = 6 TB/s (the partial writes overlap the GEMM).
+//   * a split adds the reduction kernel and the partial round trip,
+//     G + (partial bytes the reduction reads) / W with G = 7.5 us and
+//     W = 6 TB/s.
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -220,8 +226,8 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, bool vector_loads)
 {
     const CfgInfo& ci = kCfg[c];
     const double rate = p.dtype == SBX_F32 ? 0.55e12 : 0.275e12;
-    const double F = 8e-6, G = 2.5e-6, W = 6e12;
-    const double e1 = vector_loads ? 0.95 : 0.85;
+    const double F = 4e-6, G = 7.5e-6, W = 6e12;
+    const double e1 = vector_loads ? 0.9 : 0.85;
     const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
     const double w = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // one whole tile
     const int64_t P = ci.per_cu;
@@ -318,6 +324,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan p
         return launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_128x128:
         return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+    case F32_128x128_O3:
+        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 3>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_128x64:
         return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
     case F32_64x128:
@@ -355,7 +363,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     Cfg cfg = GENERIC;
     SplitPlan sp{0, 1, 0};
     if (algo != SBX_ALGO_GENERIC) {
-        Cfg cands[3];
+        Cfg cands[4];
         const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cands);
         const int64_t cus = cu_count();
         bool any = false;

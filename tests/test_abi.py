@@ -84,10 +84,10 @@ def test_noop_cases_need_no_device():
 
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w2x2"),
-    (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2+splitk2"),
+    (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
     (0, 0, 0, 0, 512, 512, 512, "mfma_f32_128x64x32_w2x2+splitk8"),
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
-    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x128x32_w2x2+splitk5"),
+    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x128x32_w2x2"),
     (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
@@ -107,6 +107,9 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (2048, 2048, 2048, "mfma_f32_128x64x32_w2x2"),             # one full round of 512 slots
     (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
+    (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
+    (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
+    (4096, 4096, 1024, "mfma_f32_256x256x32_w2x2"),
 ])
 def test_model_based_selection(m, n, k, expect):
     """Tile shape and split from the cost model (whole rounds unsplit, the

@@ -311,6 +311,29 @@ def test_deep_forward_pass_closed_form(cuda):
         assert rel < 6.2e-5 * layer, (layer, rel)
 
 
+# -- three workgroups per CU --------------------------------------------------
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
+    """The 128x128 fp32 tile compiled for three workgroups per CU: 768 ragged
+    tiles in one round (scalar loads, odd ld) and, at 3584^2 x 512, a full
+    round plus a tail split six ways."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k, beta) in enumerate([(4095, 3001, 96, 1.0), (3584, 3584, 512, 0.5)]):
+        sa = (k, m) if ta else (m, k)
+        sbd = (n, k) if tb else (k, n)
+        lda = sa[1] if layout == 0 else sa[0]
+        ldb = sbd[1] if layout == 0 else sbd[0]
+        ldc = n if layout == 0 else m
+        name = sbx.gemm_select(sbx.F32, layout, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"three-per-CU case {m}x{n}x{k} -> {name}", flush=True)
+        if i == 1:
+            assert name == "mfma_f32_128x128x16_w2x2_o3+splitk6", name
+        err, _, _ = _case(cuda, np.float32, layout, ta, tb, m, n, k, 1.0, beta, SEED + 60 + i)
+        assert err <= TOL[np.float32], (m, n, k, name)
+
+
 # -- split-K of under-filled grids ---------------------------------------------
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
