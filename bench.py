@@ -95,11 +95,16 @@ def read_traffic(workload):
     path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
     if not os.path.exists(path):
         return None
+    col = None
     for line in open(path):
+        if not line.startswith("|"):
+            continue
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 2 and cells[0] == workload:
+        if col is None and "traffic bytes" in cells:
+            col = cells.index("traffic bytes")
+        elif col is not None and len(cells) > col and cells[0] == workload:
             try:
-                return int(cells[-1])
+                return int(cells[col].replace(",", ""))
             except ValueError:
                 return None
     return None
@@ -277,7 +282,8 @@ def run_syrk_config(dtype, n, k, seed, steps, warmup):
     ms = time_launches(step, steps, warmup)
     flops = float(n) * (n + 1) * k
     tflops = flops / (ms * 1e-3) / 1e12
-    out = {"kernel": "mfma triangle tiles", "ms": round(ms, 4), "tflops": round(tflops, 3),
+    out = {"kernel": sbx.syrk_select(sdt, 0, 0, 0, n, k, k, n) + " (triangle tiles)",
+           "ms": round(ms, 4), "tflops": round(tflops, 3),
            "pct_peak": round(100 * tflops / PEAK[dtype], 2)}
     del A, C
     torch.cuda.empty_cache()

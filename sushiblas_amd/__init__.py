@@ -94,6 +94,9 @@ def lib() -> ctypes.CDLL:
     L.sbx_gemm_select.restype = i32
     L.sbx_gemm_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64,
                                   ctypes.c_char_p, ctypes.c_size_t]
+    L.sbx_syrk_select.restype = i32
+    L.sbx_syrk_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, ctypes.c_char_p,
+                                  ctypes.c_size_t]
     L.sbx_status_string.restype = ctypes.c_char_p
     L.sbx_status_string.argtypes = [i32]
     L.sbx_fill_uniform.restype = i32
@@ -201,6 +204,14 @@ def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc) -> str:
     buf = ctypes.create_string_buffer(128)
     _check(lib().sbx_gemm_select(dtype, layout, int(transA), int(transB), m, n, k, lda, ldb,
                                  ldc, buf, 128), "sbx_gemm_select")
+    return buf.value.decode()
+
+
+def syrk_select(dtype, layout, upper, trans, n, k, lda, ldc) -> str:
+    """Kernel (and split) sbx_{s,d}syrk would run for this problem."""
+    buf = ctypes.create_string_buffer(128)
+    _check(lib().sbx_syrk_select(dtype, layout, int(upper), int(trans), n, k, lda, ldc, buf, 128),
+           "sbx_syrk_select")
     return buf.value.decode()
 
 

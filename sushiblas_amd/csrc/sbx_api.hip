@@ -87,9 +87,12 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
             out[0] = F64_128x128;
             return 1;
         }
+        int c = 0;
         const int64_t t = cdiv(n, 256);
-        out[0] = t * (t + 1) / 2 >= 256 ? F32_256x256 : F32_128x128;
-        return 1;
+        if (t * (t + 1) / 2 >= 256) out[c++] = F32_256x256;
+        out[c++] = F32_128x128;
+        out[c++] = F32_128x128_O3;
+        return c;
     }
     const bool f32 = dtype == SBX_F32;
     const Cfg sq = f32 ? F32_128x128 : F64_128x128;
@@ -552,7 +555,8 @@ int grouped_impl(void* stream, int dtype, int layout, int transA, int transB, in
 // and a column-major n x k A is a row-major k x n one).
 int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
               const void* alpha, const void* A, int64_t lda, int64_t str_a, const void* beta,
-              void* C, int64_t ldc, int64_t str_c, int64_t batch)
+              void* C, int64_t ldc, int64_t str_c, int64_t batch, Cfg* chosen = nullptr,
+              SplitPlan* chosen_split = nullptr)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
@@ -588,9 +592,9 @@ int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, SBX_ALGO_AUTO, s,
-                          nullptr, nullptr);
+                          chosen, chosen_split);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, SBX_ALGO_AUTO, s,
-                       nullptr, nullptr);
+                       chosen, chosen_split);
 }
 
 // GEMV: y = alpha * op(A) x + beta * y (oneMKL gemv, gemv.cpp:44-61), netlib
@@ -809,6 +813,26 @@ int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, in
     int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda, 0,
                             fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO,
                             SBX_EPILOGUE_NONE, &cfg, &sp);
+    if (st != SBX_OK) return st;
+    if (sp.split > 1)
+        snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);
+    else
+        snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
+    return SBX_OK;
+}
+
+int sbx_syrk_select(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
+                    int64_t lda, int64_t ldc, char* name, size_t cap)
+{
+    if (!name || cap == 0) return SBX_INVALID_ARGUMENT;
+    static const float one_f = 1.0f;
+    static const double one_d = 1.0;
+    const void* one = dtype == SBX_F64 ? (const void*)&one_d : (const void*)&one_f;
+    const void* fake = (const void*)(uintptr_t)0x1000;
+    sbx::Cfg cfg = sbx::GENERIC;
+    sbx::SplitPlan sp{0, 1, 0};
+    int st = sbx::syrk_impl((void*)-1, dtype, layout, upper, trans, n, k, one, fake, lda, 0, one,
+                            (void*)fake, ldc, 0, 1, &cfg, &sp);
     if (st != SBX_OK) return st;
     if (sp.split > 1)
         snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);

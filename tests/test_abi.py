@@ -118,6 +118,20 @@ def test_model_based_selection(m, n, k, expect):
     assert sbx.gemm_select(0, 0, 0, 0, m, n, k, k, n, n) == expect
 
 
+@pytest.mark.parametrize("dtype,n,k,expect", [
+    (0, 8192, 8192, "mfma_f32_128x128x16_w2x2+splitk6"),   # 2080 triangle tiles: 4 rounds + tail
+    (0, 5000, 5000, "mfma_f32_128x128x16_w2x2+splitk3"),
+    (1, 8192, 8192, "mfma_f64_128x128x16_w2x2+splitk6"),
+])
+def test_syrk_selection(dtype, n, k, expect):
+    """SYRK picks among the square tiles with the same cost model, counting
+    only the tiles that meet the triangle; each fp32 pick was timed on the
+    device against the 256x256 and three-per-CU alternatives."""
+    assert sbx.syrk_select(dtype, 0, 0, 0, n, k, k, n) == expect
+    # column-major upper with A transposed is the same problem
+    assert sbx.syrk_select(dtype, 1, 1, 1, n, k, k, n) == expect
+
+
 def test_huge_leading_dimension_falls_back_to_generic():
     """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \

@@ -1,0 +1,40 @@
+"""Host-side parts of bench.py's contract (no GPU): the multi-GPU refusal and
+the HBM-traffic figures it reads from the committed rocprofv3 summary."""
+import os
+import re
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_traffic_is_read_from_the_bytes_column():
+    """roofline.traffic is the measured bytes per launch: FETCH_SIZE and
+    WRITE_SIZE (KiB) scaled by the copy-kernel factors of the same file."""
+    import bench
+    text = open(os.path.join(ROOT, "profiles", "hbm_traffic.md")).read()
+    m = re.search(r"FETCH_SIZE is scaled by ([0-9.]+) and WRITE_SIZE by ([0-9.]+)", text)
+    ff, fw = float(m.group(1)), float(m.group(2))
+    rows = {}
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if line.startswith("|") and len(cells) == 7 and cells[2][:1].isdigit():
+            rows[cells[0]] = cells
+    assert "headline" in rows
+    for workload, cells in rows.items():
+        got = bench.read_traffic(workload)
+        fetch, write = (float(c.replace(",", "")) for c in cells[2:4])
+        algorithmic = int(cells[4].replace(",", ""))
+        assert isinstance(got, int)
+        # the KiB columns are rounded averages: agree to 0.1 %
+        assert abs(got - (fetch * ff + write * fw) * 1024) <= 1e-3 * got + 4096, workload
+        assert abs(got / algorithmic - float(cells[6])) < 0.006, workload
+    assert bench.read_traffic("no_such_workload") is None

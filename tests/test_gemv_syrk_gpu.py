@@ -211,9 +211,11 @@ def test_syrk_known_answers(cuda):
     assert dC.cpu().tolist() == [14, 32, 0, 77]
 
 
-# (n, k): 128x128 tiles with split-K tails, 256x256 tiles (fp32, >= 256
-# triangle tiles), ragged edges, tiny sizes
-SYRK_CASES = [(1, 1), (3, 2), (130, 257), (1000, 300), (2048, 512), (4100, 64), (8192, 32)]
+# (n, k): 128x128 tiles with split-K tails, the three-per-CU 128x128 tile
+# whole (4416) and with a split tail (4928), 256x256 tiles (7680; fp32
+# only), ragged edges, tiny sizes
+SYRK_CASES = [(1, 1), (3, 2), (130, 257), (1000, 300), (2048, 512), (4100, 64), (4416, 256),
+              (4928, 256), (7680, 32)]
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
@@ -221,9 +223,14 @@ SYRK_CASES = [(1, 1), (3, 2), (130, 257), (1000, 300), (2048, 512), (4100, 64), 
 @pytest.mark.parametrize("upper", [0, 1])
 @pytest.mark.parametrize("trans", [0, 1])
 def test_syrk_matches_oracle(cuda, dtype, layout, upper, trans):
+    import sushiblas_amd as sbx
     for i, (n, k) in enumerate(SYRK_CASES):
         if dtype == np.float64 and n > 4100:
             continue
+        lda = (n if trans else k) if layout == 0 else (k if trans else n)
+        sdt = sbx.F32 if dtype == np.float32 else sbx.F64
+        print(f"syrk case {n}x{k}: {sbx.syrk_select(sdt, layout, upper, trans, n, k, lda, n)}",
+              flush=True)
         got, want, C0 = run_syrk(cuda, dtype, layout, upper, trans, n, k, 0.5, 1.5, SEED + i,
                                  sentinel=n <= 1000)
         if n <= 1000:
