@@ -116,8 +116,8 @@ int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, 
  * beta*C_i) with one shape, one set of leading dimensions and scalars, and
  * operands anywhere in device memory: `table` is a DEVICE array of 3*count
  * pointers (A_0, B_0, C_0, A_1, B_1, C_1, ...), read by the kernel in stream
- * order.  aligned16 != 0 promises every pointer is 16-byte aligned (enables
- * 16-byte loads).  One launch for all of them.  No single counterpart in the
+ * order.  aligned16 != 0 promises every C pointer is 16-byte aligned (enables
+ * 16-byte C stores; operand loads are 16 bytes at any alignment).  One launch for all of them.  No single counterpart in the
  * reference: it is how the task graph issues a run of independent,
  * same-shaped Level3::gemm tasks (each one gemm.cpp:63 / :76 call in the
  * reference, run on worker threads) without one launch per task. */

@@ -4,5 +4,5 @@
 
 namespace sbx {
 template hipError_t launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(
-    const GemmArgs<float>&, bool, bool, bool, bool, int, hipStream_t);
+    const GemmArgs<float>&, bool, bool, int, hipStream_t);
 }  // namespace sbx

@@ -4,5 +4,5 @@
 
 namespace sbx {
 template hipError_t launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(
-    const GemmArgs<float>&, bool, bool, bool, bool, int, hipStream_t);
+    const GemmArgs<float>&, bool, bool, int, hipStream_t);
 }  // namespace sbx

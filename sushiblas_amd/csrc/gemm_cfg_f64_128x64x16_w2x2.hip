@@ -4,5 +4,5 @@
 
 namespace sbx {
 template hipError_t launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(
-    const GemmArgs<double>&, bool, bool, bool, bool, int, hipStream_t);
+    const GemmArgs<double>&, bool, bool, int, hipStream_t);
 }  // namespace sbx

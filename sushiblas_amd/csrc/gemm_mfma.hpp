@@ -20,9 +20,12 @@
 //    x-contiguous tile, U neighbouring MFMA blocks are interleaved (block u
 //    owns rows U*i + u) so that one 16-byte read feeds U blocks.
 //  * Masking: loads go through buffer resources whose base moves with the
-//    tile; an element outside [0,M)x[0,K) (or [0,K)x[0,N)) gets the offset
-//    0x80000000, which the buffer unit turns into a zero.  Ragged M/N/K and
-//    unaligned leading dimensions (vector width 1) need no separate kernel.
+//    tile; a vector that starts outside [0,M)x[0,K) (or [0,K)x[0,N)) gets
+//    the offset 0x80000000, which the buffer unit turns into zeros.  Every
+//    load is 16 bytes, also for odd leading dimensions (4/8-byte aligned
+//    addresses); a k-contiguous vector that straddles K is zeroed past K
+//    before its LDS write.  Ragged M/N/K and unaligned leading dimensions
+//    need no separate kernel.
 //  * LDS is double-buffered: the global loads for tile t+1 are issued before
 //    the MFMAs of tile t, stored to the other LDS buffer after them, and one
 //    barrier per k-tile separates producer and consumer.
@@ -90,33 +93,15 @@ struct Mfma<double> {
     __device__ static inline int row(int r, int q) { return q + 4 * r; }
 };
 
-// Raw buffer loads of 4/8/16 bytes.
-template <int BYTES>
-struct Raw;
-template <>
-struct Raw<4> {
-    typedef uint32_t type;
-    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
-    {
-        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    }
-};
-template <>
-struct Raw<8> {
-    typedef u32x2 type;
-    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
-    {
-        return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-    }
-};
-template <>
-struct Raw<16> {
-    typedef u32x4 type;
-    __device__ static inline type load(__amdgpu_buffer_rsrc_t r, int off)
-    {
-        return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    }
-};
+// Raw 16-byte buffer load.  The byte offset need only be 4-byte aligned:
+// gfx950 serves unaligned multi-dword buffer loads (the device runs in
+// unaligned access mode), and range-checks each dword on its own, so a load
+// that straddles the end of the resource returns its in-range dwords and
+// zeros for the rest (both checked on the device with in-bounds probes).
+__device__ inline u32x4 raw_load16(__amdgpu_buffer_rsrc_t r, int off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 
 // Typed N-element LDS vector read (N * sizeof(T) in {4, 8, 16}).
 template <typename T, int N>
@@ -272,14 +257,16 @@ __device__ inline T relu_of(T x)
 }
 
 // ---------------------------------------------------------------------------
-// One operand's global -> LDS pipeline.
+// One operand's global -> LDS pipeline, in 16-byte vectors (VEC elements)
+// whatever the alignment of the leading dimension and base.
 //   KC: the operand's k index is contiguous in memory (tile [X][BK+PAD]).
 //   X : tile extent along m (for A) or n (for B).
-//   VEC: elements per global load (1, or 16 bytes / sizeof(T)).
+//   KTAIL: K is not a multiple of VEC, so a k-contiguous vector may straddle K.
 // ---------------------------------------------------------------------------
-template <typename T, int X, int BK, bool KC, int VEC, int PF>
+template <typename T, int X, int BK, bool KC, int PF, bool KTAIL>
 struct Operand {
     static constexpr int V = 16 / (int)sizeof(T);
+    static constexpr int VEC = V;  // elements per global load
     static constexpr int PAD = KC ? V : 0;
     static constexpr int LD = KC ? BK + PAD : X + PAD;          // LDS row pitch (elements)
     static constexpr int ELEMS = KC ? X * LD : BK * LD;         // LDS tile size (elements)
@@ -287,13 +274,14 @@ struct Operand {
     static constexpr int VPR = CONTIG / VEC;                     // vectors per tile row
     static constexpr int NV = X * BK / (VEC * 256);              // vectors per thread
     static_assert(X * BK % (VEC * 256) == 0, "tile not divisible over 256 lanes");
-    typedef typename Raw<VEC * sizeof(T)>::type raw_t;
+    typedef u32x4 raw_t;
 
     int off[NV];       // byte offset of each vector relative to the tile base
     int lds_off[NV];   // element offset in the LDS tile
     int kidx[NV];      // k index of each vector within the tile
     bool xok[NV];      // row/column validity along X (fixed for the block)
     raw_t stage[PF][NV];  // register staging, PF tiles in flight
+    int krem[PF];      // k extent left at the staged tile (k-tail masking)
 
     __device__ inline void init(int tid, int64_t ld, int x_rem)
     {
@@ -320,15 +308,31 @@ struct Operand {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             bool ok = xok[j] && kidx[j] < k_rem;
-            stage[S][j] = Raw<VEC * sizeof(T)>::load(rs, ok ? off[j] : kOobOffset);
+            stage[S][j] = raw_load16(rs, ok ? off[j] : kOobOffset);
         }
+        krem[S] = k_rem;
     }
 
+    // A k-contiguous vector that straddles K holds, past K, the first
+    // elements of the next row (or zeros past the buffer's end: the range
+    // check is per dword): zero them.  An x-contiguous vector that straddles
+    // the X extent needs nothing -- those elements only reach C rows/columns
+    // that are never stored -- and its k index is one row, checked at load.
     template <int S>
     __device__ inline void store(T* lds)
     {
+        constexpr int DPE = (int)sizeof(T) / 4;  // dwords per element
 #pragma unroll
-        for (int j = 0; j < NV; ++j) *reinterpret_cast<raw_t*>(lds + lds_off[j]) = stage[S][j];
+        for (int j = 0; j < NV; ++j) {
+            raw_t w = stage[S][j];
+            if constexpr (KC && KTAIL) {
+                const int lim = krem[S] - kidx[j];  // elements of vector j inside K
+#pragma unroll
+                for (int d = DPE; d < VEC * DPE; ++d)
+                    w[d] = d / DPE < lim ? w[d] : 0u;
+            }
+            *reinterpret_cast<raw_t*>(lds + lds_off[j]) = w;
+        }
     }
 };
 
@@ -430,7 +434,7 @@ using Int = std::integral_constant<int, N>;
 // one is multiplied; 2 = the one after that too, for HBM-bound shapes).
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          int VA, int VB, int PF, int WPE>
+          bool KTAIL, int PF, int WPE>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
@@ -443,8 +447,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
     static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
     static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
     static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
-    typedef Operand<T, BM, BK, A_KC, VA, PF> OpA;
-    typedef Operand<T, BN, BK, B_KC, VB, PF> OpB;
+    typedef Operand<T, BM, BK, A_KC, PF, KTAIL> OpA;
+    typedef Operand<T, BN, BK, B_KC, PF, KTAIL> OpB;
     typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
     typedef Frag<T, NBN, B_KC, OpB::LD> FragB;
 

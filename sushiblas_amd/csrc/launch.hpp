@@ -1,8 +1,9 @@
 // launch.hpp -- host-side launchers for the GEMM kernels.
 //
-// launch_mfma<T, BM, BN, BK, WAVES_M, WAVES_N> picks one of the 16 compiled
-// variants (A k-contiguous or not, B k-contiguous or not, vector or scalar
-// global loads for each operand) and launches it on `stream`.
+// launch_mfma<T, BM, BN, BK, WAVES_M, WAVES_N, PF, WPE> picks one of the 7
+// compiled variants (A k-contiguous or not, B k-contiguous or not, and for a
+// k-contiguous operand whether K needs tail masking) and launches it on
+// `stream`.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,8 +13,7 @@
 namespace sbx {
 
 template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
-hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, bool b_vec,
-                       int batch, hipStream_t stream);
+hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream);
 
 // Generic (non-MFMA) fallback: 64x64 tiles, 64-bit addressing, any ld.
 template <typename T>
@@ -47,7 +47,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 
 #define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN, PF, WPE)                                        \
     extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN, PF, WPE>(                         \
-        const GemmArgs<T>&, bool, bool, bool, bool, int, hipStream_t);
+        const GemmArgs<T>&, bool, bool, int, hipStream_t);
 SBX_MFMA_CONFIGS(SBX_EXTERN_LAUNCH)
 #undef SBX_EXTERN_LAUNCH
 

@@ -1,7 +1,6 @@
 // launch_mfma_impl.hpp -- definition of launch_mfma (see launch.hpp).  Only
 // the gemm_cfg_*.hip translation units include this, each instantiating one
-// tile configuration, so the 16 kernel variants per configuration compile in
-// parallel.
+// tile configuration, so the configurations compile in parallel.
 #pragma once
 
 #include "launch.hpp"
@@ -9,33 +8,27 @@
 namespace sbx {
 
 template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
-hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, bool a_vec, bool b_vec,
-                       int batch, hipStream_t stream)
+hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream)
 {
-    constexpr int V = 16 / (int)sizeof(T);
     const int tiles = a.tiles;
     const dim3 grid((unsigned)(a.num_full + (tiles - a.num_full) * a.split), 1, (unsigned)batch);
     const dim3 block(256);
-    const int sel = (a_kc ? 8 : 0) | (b_kc ? 4 : 0) | (a_vec ? 2 : 0) | (b_vec ? 1 : 0);
-#define SBX_LAUNCH(AK, BKC, VA, VB) \
-    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, VA, VB, PF, WPE><<<grid, block, 0, stream>>>(a)
-    switch (sel) {
-    case 0: SBX_LAUNCH(false, false, 1, 1); break;
-    case 1: SBX_LAUNCH(false, false, 1, V); break;
-    case 2: SBX_LAUNCH(false, false, V, 1); break;
-    case 3: SBX_LAUNCH(false, false, V, V); break;
-    case 4: SBX_LAUNCH(false, true, 1, 1); break;
-    case 5: SBX_LAUNCH(false, true, 1, V); break;
-    case 6: SBX_LAUNCH(false, true, V, 1); break;
-    case 7: SBX_LAUNCH(false, true, V, V); break;
-    case 8: SBX_LAUNCH(true, false, 1, 1); break;
-    case 9: SBX_LAUNCH(true, false, 1, V); break;
-    case 10: SBX_LAUNCH(true, false, V, 1); break;
-    case 11: SBX_LAUNCH(true, false, V, V); break;
-    case 12: SBX_LAUNCH(true, true, 1, 1); break;
-    case 13: SBX_LAUNCH(true, true, 1, V); break;
-    case 14: SBX_LAUNCH(true, true, V, 1); break;
-    default: SBX_LAUNCH(true, true, V, V); break;
+    // k-tail masking is compiled in only where a k-contiguous operand meets a
+    // K that is not a multiple of the 16-byte vector (it costs 1-4 %)
+    const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
+#define SBX_LAUNCH(AK, BKC, TAIL) \
+    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE><<<grid, block, 0, stream>>>(a)
+    if (a_kc && b_kc) {
+        if (tail) SBX_LAUNCH(true, true, true);
+        else SBX_LAUNCH(true, true, false);
+    } else if (a_kc) {
+        if (tail) SBX_LAUNCH(true, false, true);
+        else SBX_LAUNCH(true, false, false);
+    } else if (b_kc) {
+        if (tail) SBX_LAUNCH(false, true, true);
+        else SBX_LAUNCH(false, true, false);
+    } else {
+        SBX_LAUNCH(false, false, false);
     }
 #undef SBX_LAUNCH
     if (a.split > 1) {

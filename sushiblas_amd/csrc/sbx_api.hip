@@ -44,7 +44,8 @@ struct Problem {
     int uplo;  // 0: whole C; 1 / 2: lower / upper triangle only (SYRK, B == A, m == n)
     // grouped launch: batch entry z's A, B, C come from this device table
     // (3 pointers per entry); A/B/C above are then 16-byte aligned (or not)
-    // stand-in addresses that only carry the alignment facts
+    // stand-in addresses that only carry the alignment fact C's vector
+    // stores need
     const void* const* table;
     int table_swap;
 };
@@ -118,23 +119,6 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
     return c;
 }
 
-// Row-major operand facts for the MFMA kernels.
-//   A (m x k): k-contiguous iff not transposed; contiguous extent k or m.
-//   B (k x n): k-contiguous iff transposed;     contiguous extent k or n.
-struct OperandPlan {
-    bool kc;
-    bool vec;
-};
-
-OperandPlan plan_operand(bool kc, int64_t contig_extent, int64_t ld, int64_t stride,
-                         int64_t batch, const void* ptr, size_t elem)
-{
-    const int64_t V = 16 / (int64_t)elem;
-    bool vec = (contig_extent % V == 0) && (ld % V == 0) &&
-               ((uintptr_t)ptr % 16 == 0) && (batch <= 1 || stride % V == 0);
-    return OperandPlan{kc, vec};
-}
-
 // Largest byte offset an MFMA tile forms relative to its buffer base.
 bool offsets_fit(bool kc, int tile_x, int bk, int64_t ld, size_t elem)
 {
@@ -170,9 +154,8 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     (fp32; 0.275 fp64);
 //   * a config keeps P workgroups per CU (its waves per SIMD); a round of
 //     P*CUs workgroups takes P*w; a partial round whose busiest CU holds
-//     q < P workgroups takes q*w/e1, where e1 is what a CU achieves short of
-//     its co-resident partners (0.9 with 16-byte loads, 0.85 when an operand
-//     needs scalar loads);
+//     q < P workgroups takes q*w/e1, where e1 = 0.9 is what a CU achieves
+//     short of its co-resident partners;
 //   * the grid adds F = 4 us once (pipeline fill and the last epilogue; in
 //     between, co-resident workgroups hide each other's);
 //   * a split adds the reduction kernel and the partial round trip,
@@ -225,12 +208,12 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
     return t;
 }
 
-Choice model_plan(const Problem& p, Cfg c, int64_t cus, bool vector_loads)
+Choice model_plan(const Problem& p, Cfg c, int64_t cus)
 {
     const CfgInfo& ci = kCfg[c];
     const double rate = p.dtype == SBX_F32 ? 0.55e12 : 0.275e12;
     const double F = 4e-6, G = 7.5e-6, W = 6e12;
-    const double e1 = vector_loads ? 0.9 : 0.85;
+    const double e1 = 0.9;
     const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
     const double w = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // one whole tile
     const int64_t P = ci.per_cu;
@@ -319,20 +302,20 @@ WorkspaceLease stream_workspace(hipStream_t stream, size_t bytes)
     return lease;
 }
 
-hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan pb,
-                      const Problem& p, int nb, hipStream_t s)
+hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Problem& p,
+                      int nb, hipStream_t s)
 {
     switch (cfg) {
     case F32_256x256:
-        return launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(a, akc, bkc, nb, s);
     case F32_128x128:
-        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_128x128_O3:
-        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 3>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 128, 128, 16, 2, 2, 2, 3>(a, akc, bkc, nb, s);
     case F32_128x64:
-        return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_64x128:
-        return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -340,16 +323,16 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, OperandPlan pa, OperandPlan p
     }
 }
 
-hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, OperandPlan pa, OperandPlan pb,
-                      const Problem& p, int nb, hipStream_t s)
+hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Problem& p,
+                      int nb, hipStream_t s)
 {
     switch (cfg) {
     case F64_128x128:
-        return launch_mfma<double, 128, 128, 16, 2, 2, 1, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<double, 128, 128, 16, 2, 2, 1, 2>(a, akc, bkc, nb, s);
     case F64_128x64:
-        return launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F64_64x128:
-        return launch_mfma<double, 64, 128, 16, 2, 2, 2, 2>(a, pa.kc, pb.kc, pa.vec, pb.vec, nb, s);
+        return launch_mfma<double, 64, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -371,12 +354,9 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         const int64_t cus = cu_count();
         bool any = false;
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
-        const size_t el = p.dtype == SBX_F32 ? 4 : 8;
-        const bool vec = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch, p.A, el).vec &&
-                         plan_operand(p.tb, p.tb ? p.k : p.n, p.ldb, p.str_b, p.batch, p.B, el).vec;
         for (int i = 0; i < nc; ++i) {
             if (!mfma_feasible(p, cands[i])) continue;
-            const Choice c = model_plan(p, cands[i], cus, vec);
+            const Choice c = model_plan(p, cands[i], cus);
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;
         }
@@ -429,12 +409,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.tiles = (int)tiles;
             a.table = p.table ? p.table + 3 * b0 : nullptr;
             a.table_swap = p.table_swap;
-            const size_t elem = sizeof(T);
-            const OperandPlan pa = plan_operand(!p.ta, p.ta ? p.m : p.k, p.lda, p.str_a, p.batch,
-                                                a.A, elem);
-            const OperandPlan pb = plan_operand(p.tb, p.tb ? p.k : p.n, p.ldb, p.str_b, p.batch,
-                                                a.B, elem);
-            e = launch_cfg(cfg, a, pa, pb, p, nb, stream);
+            // A (m x k) is k-contiguous iff not transposed, B (k x n) iff transposed
+            e = launch_cfg(cfg, a, !p.ta, p.tb != 0, p, nb, stream);
         }
         if (e != hipSuccess) return SBX_HIP_ERROR;
     }

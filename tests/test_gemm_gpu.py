@@ -170,7 +170,7 @@ def test_generic_path_matches(cuda, dtype, ta, tb):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_padded_ld_and_unaligned_pointers(cuda, dtype):
     """ld larger than the minimum and base pointers off 16-byte alignment
-    (forces the scalar-load variants)."""
+    (16-byte operand loads at 4/8-byte aligned addresses)."""
     for ta, tb in [(0, 0), (1, 0), (0, 1), (1, 1)]:
         err, _, _ = _case(cuda, dtype, 0, ta, tb, 260, 196, 132, 1.0, 0.5, SEED + 40,
                           pad=(3, 5, 7), offsets=(1, 3, 1))
@@ -178,6 +178,44 @@ def test_padded_ld_and_unaligned_pointers(cuda, dtype):
         err, _, _ = _case(cuda, dtype, 0, ta, tb, 256, 256, 128, 1.0, 0.0, SEED + 41,
                           pad=(4, 8, 4))
         assert err <= TOL[dtype]
+
+
+def _poison_padding(X, layout, sr, sc, ld):
+    """Set every element of a stored sr x sc matrix's buffer that lies outside
+    the matrix (the ld padding) to NaN."""
+    idx = np.arange(X.size)
+    inner = idx % ld < (sc if layout == 0 else sr)
+    X[~inner] = np.nan
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_vector_loads_past_k_and_edges_ignore_padding(cuda, dtype, layout, ta, tb):
+    """Operands are read in 16-byte vectors at any alignment.  A vector that
+    straddles K reads the ld padding (NaN here) and must zero it; one that
+    straddles M or N feeds only C entries that are never stored.  Odd K,
+    padded ld, bases off 16-byte alignment, every tile shape."""
+    from gemm_cases import stored_dims
+    shapes = [(129, 67, 37), (300, 257, 301), (1001, 63, 303), (61, 1003, 305), (130, 67, 64)]
+    if dtype == np.float32:
+        shapes.append((4095, 3001, 97))  # three-per-CU 128x128 tile
+    for i, (m, n, k) in enumerate(shapes):
+        A, lda, B, ldb, C, ldc = make_inputs(dtype, layout, ta, tb, m, n, k, SEED + 45 + i,
+                                             pad=(3, 1, 2))
+        _poison_padding(A, layout, *stored_dims(ta, m, k), lda)
+        _poison_padding(B, layout, *stored_dims(tb, k, n), ldb)
+        got = run_sbx(cuda, dtype, layout, ta, tb, m, n, k, 1.0, A, lda, B, ldb, 0.5, C, ldc,
+                      offsets=(1, 3, 1))
+        want = run_oracle(layout, ta, tb, m, n, k, 1.0, A, lda, B, ldb, 0.5, C, ldc)
+        gw, ww = c_window(layout, got, m, n, ldc), c_window(layout, want, m, n, ldc)
+        print(f"padding-NaN case {np.dtype(dtype).name} layout={layout} t{ta}{tb} {m}x{n}x{k}",
+              flush=True)
+        assert np.isfinite(gw).all(), (m, n, k)
+        assert oracle.rel_fro_err(gw, ww) <= TOL[dtype], (m, n, k)
+        # C's own padding is never written
+        cpad = np.arange(C.size) % ldc >= (n if layout == 0 else m)
+        np.testing.assert_array_equal(got[cpad], C[cpad])
 
 
 # -- BLAS edge semantics ------------------------------------------------------
