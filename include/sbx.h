@@ -87,8 +87,17 @@ int sbx_dgemm_strided_batched(void* stream, int layout, int transA, int transB, 
 
 /* Algorithm override for tests and tuning (no counterpart in the reference,
  * where oneMKL chooses internally): SBX_ALGO_AUTO is what the four entry
- * points above use. */
-typedef enum sbx_algo { SBX_ALGO_AUTO = 0, SBX_ALGO_GENERIC = 1, SBX_ALGO_MFMA = 2 } sbx_algo;
+ * points above use.  SBX_ALGO_MFMA: any MFMA kernel (model's choice);
+ * SBX_ALGO_MFMA_TILE: the LDS-tiled MFMA kernels only; SBX_ALGO_MFMA_SMALL:
+ * the one-launch small-problem kernel (fp32 only).  A forced choice the
+ * problem cannot use returns SBX_UNSUPPORTED. */
+typedef enum sbx_algo {
+    SBX_ALGO_AUTO = 0,
+    SBX_ALGO_GENERIC = 1,
+    SBX_ALGO_MFMA = 2,
+    SBX_ALGO_MFMA_TILE = 3,
+    SBX_ALGO_MFMA_SMALL = 4
+} sbx_algo;
 
 /* dtype-generic form of the four entry points above; alpha/beta point to a
  * float (SBX_F32) or double (SBX_F64). */

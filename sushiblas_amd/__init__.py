@@ -19,7 +19,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsbx.so")
 
 F32, F64 = 0, 1
-ALGO_AUTO, ALGO_GENERIC, ALGO_MFMA = 0, 1, 2
+ALGO_AUTO, ALGO_GENERIC, ALGO_MFMA, ALGO_MFMA_TILE, ALGO_MFMA_SMALL = 0, 1, 2, 3, 4
 EPILOGUE_NONE, EPILOGUE_RELU = 0, 1
 STATUS = {0: "SBX_OK", 1: "SBX_INVALID_ARGUMENT", 2: "SBX_UNSUPPORTED", 3: "SBX_HIP_ERROR"}
 

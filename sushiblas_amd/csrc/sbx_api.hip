@@ -60,6 +60,7 @@ enum Cfg {
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
     F64_64x128,
+    F32_SMALL,     // small fp32: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
     GENERIC,
 };
 
@@ -74,7 +75,8 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
-    {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"generic_64x64x16", 64, 64, 16, 4},
+    {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
+    {"generic_64x64x16", 64, 64, 16, 4},
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -99,23 +101,20 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
     const Cfg sq = f32 ? F32_128x128 : F64_128x128;
     const Cfg tall = f32 ? F32_128x64 : F64_128x64;   // n <= 64 (tall-skinny)
     const Cfg wide = f32 ? F32_64x128 : F64_64x128;   // m <= 64
-    if (n <= 64) {
-        out[0] = tall;
-        return 1;
-    }
-    if (m <= 64) {
-        out[0] = wide;
-        return 1;
-    }
-    if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 256) {
-        out[0] = F32_256x256;  // full rounds of the largest tile
-        return 1;
-    }
     int c = 0;
-    out[c++] = sq;
-    if (f32) out[c++] = F32_128x128_O3;
-    out[c++] = m >= n ? tall : wide;
-    out[c++] = m >= n ? wide : tall;
+    if (n <= 64) {
+        out[c++] = tall;
+    } else if (m <= 64) {
+        out[c++] = wide;
+    } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 256) {
+        out[c++] = F32_256x256;  // full rounds of the largest tile
+    } else {
+        out[c++] = sq;
+        if (f32) out[c++] = F32_128x128_O3;
+        out[c++] = m >= n ? tall : wide;
+        out[c++] = m >= n ? wide : tall;
+    }
+    if (f32) out[c++] = F32_SMALL;
     return c;
 }
 
@@ -160,7 +159,12 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     between, co-resident workgroups hide each other's);
 //   * a split adds the reduction kernel and the partial round trip,
 //     G + (partial bytes the reduction reads) / W with G = 7.5 us and
-//     W = 6 TB/s.
+//     W = 6 TB/s;
+//   * the one-launch small-problem kernel (fp32, 32x32 tiles) takes
+//     2 us + ceil(tiles / CUs) * 2*32*32*K / Rs, Rs = 0.22 / 0.19 / 0.16
+//     TFLOP/s per CU with 2 / 1 / 0 k-contiguous operands (fitted on 28
+//     more shapes from 64^3 to 2048x2048x256; with it the pick is within
+//     0.9 % of the fastest on average over all 76 shapes).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -210,6 +214,16 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
 
 Choice model_plan(const Problem& p, Cfg c, int64_t cus)
 {
+    if (c == F32_SMALL) {
+        // one launch, no split: a CU works through its 32x32 tiles at a rate
+        // that hardly depends on how many share it (latency bound per wave);
+        // x-contiguous operands cost one 4-byte load per k step
+        const int kc = (p.ta ? 0 : 1) + (p.tb ? 1 : 0);
+        const double rate = kc == 2 ? 0.22e12 : (kc == 1 ? 0.19e12 : 0.16e12);
+        const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
+        const double t = 2e-6 + (double)cdiv(units, cus) * 2.0 * 32 * 32 * (double)p.k / rate;
+        return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
+    }
     const CfgInfo& ci = kCfg[c];
     const double rate = p.dtype == SBX_F32 ? 0.55e12 : 0.275e12;
     const double F = 4e-6, G = 7.5e-6, W = 6e12;
@@ -316,6 +330,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_64x128:
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
+    case F32_SMALL:
+        return launch_small(a, akc, bkc, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -349,18 +365,20 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     Cfg cfg = GENERIC;
     SplitPlan sp{0, 1, 0};
     if (algo != SBX_ALGO_GENERIC) {
-        Cfg cands[4];
+        Cfg cands[5];
         const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cands);
         const int64_t cus = cu_count();
         bool any = false;
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
         for (int i = 0; i < nc; ++i) {
             if (!mfma_feasible(p, cands[i])) continue;
+            if (algo == SBX_ALGO_MFMA_TILE && cands[i] == F32_SMALL) continue;
+            if (algo == SBX_ALGO_MFMA_SMALL && cands[i] != F32_SMALL) continue;
             const Choice c = model_plan(p, cands[i], cus);
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;
         }
-        if (!any && algo == SBX_ALGO_MFMA) return SBX_UNSUPPORTED;
+        if (!any && algo != SBX_ALGO_AUTO) return SBX_UNSUPPORTED;
         if (any) {
             cfg = best.cfg;
             sp = best.sp;
@@ -427,7 +445,7 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
     if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
     if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return SBX_INVALID_ARGUMENT;
-    if (algo < SBX_ALGO_AUTO || algo > SBX_ALGO_MFMA) return SBX_INVALID_ARGUMENT;
+    if (algo < SBX_ALGO_AUTO || algo > SBX_ALGO_MFMA_SMALL) return SBX_INVALID_ARGUMENT;
     if (m < 0 || n < 0 || k < 0 || batch < 0) return SBX_INVALID_ARGUMENT;
     if (m > kMaxDim || n > kMaxDim || k > kMaxDim) return SBX_UNSUPPORTED;
     if (!alpha || !beta) return SBX_INVALID_ARGUMENT;

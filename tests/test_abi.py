@@ -85,9 +85,9 @@ def test_noop_cases_need_no_device():
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w2x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
-    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_128x64x32_w2x2+splitk8"),
+    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit4"),
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
-    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_64x128x32_w2x2"),
+    (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_32x32_ksplit4"),
     (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
@@ -110,6 +110,9 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
     (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
     (4096, 4096, 1024, "mfma_f32_256x256x32_w2x2"),
+    (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
+    (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
+    (512, 512, 2048, "mfma_f32_128x64x32_w2x2+splitk8"),       # long K: the tile kernel's split
 ])
 def test_model_based_selection(m, n, k, expect):
     """Tile shape and split from the cost model (whole rounds unsplit, the
@@ -134,11 +137,17 @@ def test_syrk_selection(dtype, n, k, expect):
 
 def test_huge_leading_dimension_falls_back_to_generic():
     """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
-    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \
+    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 24, 1024, 1024) == \
         "generic_64x64x16"
-    # 2^22: 128-row tiles overflow, 64-row tiles still fit -> an MFMA kernel
+    # 2^23: only the 32-row tiles of the small-problem kernel still fit
+    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \
+        "mfma_f32_32x32_ksplit4"
+    # 2^22: 128-row tiles overflow, 64-row tiles still fit
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024).startswith(
         "mfma_f32_64x128")
+    # fp64 has no small kernel: 2^22 doubles per row is already too far for 64 rows
+    assert sbx.gemm_select(1, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
+        "generic_64x64x16"
 
 
 def test_fused_gemm_validation():

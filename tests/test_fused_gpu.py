@@ -78,13 +78,13 @@ def test_fused_relu_padded_and_unaligned(cuda):
 
 def test_fused_relu_generic_kernel(cuda):
     """A leading dimension too large for 32-bit buffer offsets in any MFMA tile
-    (64 rows x 2^23 floats spans 2 GiB): generic kernel + ReLU.  Three rows
+    (32 rows x 2^24 floats spans 2 GiB): generic kernel + ReLU.  Three rows
     keep the buffer small."""
     import sushiblas_amd as sbx
-    assert sbx.gemm_select(0, 0, 0, 0, 3, 64, 64, 1 << 23, 64, 64) == "generic_64x64x16"
+    assert sbx.gemm_select(0, 0, 0, 0, 3, 64, 64, 1 << 24, 64, 64) == "generic_64x64x16"
     import torch
     m, n, k = 3, 64, 64
-    lda = 1 << 23
+    lda = 1 << 24
     dA = torch.zeros((m - 1) * lda + k, dtype=torch.float32, device=cuda)
     A = oracle.fill_uniform(m * k, np.float32, SEED + 3, 0).reshape(m, k)
     dA.view(-1)[: (m - 1) * lda + k].as_strided((m, k), (lda, 1)).copy_(torch.from_numpy(A))
