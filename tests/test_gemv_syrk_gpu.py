@@ -90,7 +90,7 @@ def test_gemv_known_answer(cuda):
 # and without row chunks; vector and scalar loads.
 GEMV_CASES = [
     (4096, 4096), (257, 1023), (1, 100000), (100000, 1), (8192, 64), (64, 8192),
-    (64, 262144), (131072, 16), (3, 5), (1000, 300),
+    (64, 262144), (131072, 16), (3, 5), (1000, 300), (2048, 2048),
 ]
 
 
