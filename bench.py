@@ -70,13 +70,25 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n * 4, "dispatches": 3}), flush=True)
 
 
-def time_launches(fn, steps, warmup):
+def time_launches(fn, steps, warmup, min_warm_s=0.0):
     """Average device time per call of fn() over `steps` back-to-back calls,
-    measured with HIP events on the stream the kernels run on."""
+    measured with HIP events on the stream the kernels run on.
+
+    `warmup` untimed calls come first; with min_warm_s > 0, more untimed calls
+    follow until that much time has been spent warming up.  A GPU that sat
+    idle during host-side setup takes tens of milliseconds to reach its
+    working clock: the tall-skinny GEMM (0.3 ms a call) measured 380 us over
+    its first 25 calls and 307-313 us after that, on one box."""
+    import time
     import torch
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < min_warm_s:
+        for _ in range(max(1, warmup)):
+            fn()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -193,7 +205,7 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
     def step():
         sbx.gemm_ex(sdt, layout, ta, tb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0)
 
-    ms = time_launches(step, steps, warmup)
+    ms = time_launches(step, steps, warmup, min_warm_s=0.25)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     nbytes = (m * k + k * n + m * n * (2 if beta != 0 else 1)) * A.element_size()
@@ -225,8 +237,8 @@ def run_fused_config(m, n, k, seed, steps, warmup):
         sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0)
         sbx.relu(C)
 
-    ms_f = time_launches(fused, steps, warmup)
-    ms_u = time_launches(unfused, steps, warmup)
+    ms_f = time_launches(fused, steps, warmup, min_warm_s=0.25)
+    ms_u = time_launches(unfused, steps, warmup, min_warm_s=0.25)
     flops = 2.0 * m * n * k
     out = {"kernel": sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n) + "+relu",
            "ms": round(ms_f, 4), "tflops": round(flops / (ms_f * 1e-3) / 1e12, 3),
@@ -254,7 +266,7 @@ def run_gemv_config(dtype, trans, m, n, seed, steps, warmup):
     def step():
         sbx.gemv(sdt, 0, trans, m, n, 1.0, A, n, x, 1, 0.0, y, 1)
 
-    ms = time_launches(step, steps, warmup)
+    ms = time_launches(step, steps, warmup, min_warm_s=0.25)
     nbytes = (m * n + xlen + ylen) * A.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {"kernel": "gemv_cols" if trans else "gemv_rows", "ms": round(ms, 4),
@@ -279,7 +291,7 @@ def run_syrk_config(dtype, n, k, seed, steps, warmup):
     def step():
         sbx.syrk(sdt, 0, 0, 0, n, k, 1.0, A, k, 0, 0.0, C, n, 0)
 
-    ms = time_launches(step, steps, warmup)
+    ms = time_launches(step, steps, warmup, min_warm_s=0.25)
     flops = float(n) * (n + 1) * k
     tflops = flops / (ms * 1e-3) / 1e12
     out = {"kernel": sbx.syrk_select(sdt, 0, 0, 0, n, k, k, n) + " (triangle tiles)",
