@@ -89,7 +89,7 @@ int sbx_dgemm_strided_batched(void* stream, int layout, int transA, int transB, 
  * where oneMKL chooses internally): SBX_ALGO_AUTO is what the four entry
  * points above use.  SBX_ALGO_MFMA: any MFMA kernel (model's choice);
  * SBX_ALGO_MFMA_TILE: the LDS-tiled MFMA kernels only; SBX_ALGO_MFMA_SMALL:
- * the one-launch small-problem kernel (fp32 only).  A forced choice the
+ * the one-launch small-problem kernel.  A forced choice the
  * problem cannot use returns SBX_UNSUPPORTED. */
 typedef enum sbx_algo {
     SBX_ALGO_AUTO = 0,

@@ -60,7 +60,8 @@ enum Cfg {
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
     F64_64x128,
-    F32_SMALL,     // small fp32: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
+    F32_SMALL,     // small problems: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
+    F64_SMALL,
     GENERIC,
 };
 
@@ -76,7 +77,7 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
-    {"generic_64x64x16", 64, 64, 16, 4},
+    {"mfma_f64_32x32_ksplit4", 32, 32, 32, 1},     {"generic_64x64x16", 64, 64, 16, 4},
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -114,7 +115,7 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         out[c++] = m >= n ? tall : wide;
         out[c++] = m >= n ? wide : tall;
     }
-    if (f32) out[c++] = F32_SMALL;
+    out[c++] = f32 ? F32_SMALL : F64_SMALL;
     return c;
 }
 
@@ -160,11 +161,12 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //   * a split adds the reduction kernel and the partial round trip,
 //     G + (partial bytes the reduction reads) / W with G = 7.5 us and
 //     W = 6 TB/s;
-//   * the one-launch small-problem kernel (fp32, 32x32 tiles) takes
+//   * the one-launch small-problem kernel (32x32 tiles) takes
 //     2 us + ceil(tiles / CUs) * 2*32*32*K / Rs, Rs = 0.22 / 0.19 / 0.16
-//     TFLOP/s per CU with 2 / 1 / 0 k-contiguous operands (fitted on 28
-//     more shapes from 64^3 to 2048x2048x256; with it the pick is within
-//     0.9 % of the fastest on average over all 76 shapes).
+//     TFLOP/s per CU with 2 / 1 / 0 k-contiguous operands, half that for
+//     fp64 (fitted on 28 more fp32 and 28 more fp64 shapes from 64^3 to
+//     2048x2048x256; with it the pick is within 0.9 % of the fastest on
+//     average over all 104 shapes).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -212,14 +214,20 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
     return t;
 }
 
+// The fp64 small-problem kernel's rate relative to fp32's (fitted on 28
+// small fp64 shapes, 64^3 .. 2048x2048x256, with the tile kernels' splits
+// as the alternatives: the pick is within 0.9 % of the fastest on average)
+constexpr double kSmallF64Rate = 0.5;
+
 Choice model_plan(const Problem& p, Cfg c, int64_t cus)
 {
-    if (c == F32_SMALL) {
+    if (c == F32_SMALL || c == F64_SMALL) {
         // one launch, no split: a CU works through its 32x32 tiles at a rate
         // that hardly depends on how many share it (latency bound per wave);
-        // x-contiguous operands cost one 4-byte load per k step
+        // x-contiguous operands cost one element load per k step
         const int kc = (p.ta ? 0 : 1) + (p.tb ? 1 : 0);
-        const double rate = kc == 2 ? 0.22e12 : (kc == 1 ? 0.19e12 : 0.16e12);
+        double rate = kc == 2 ? 0.22e12 : (kc == 1 ? 0.19e12 : 0.16e12);
+        if (c == F64_SMALL) rate *= kSmallF64Rate;
         const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
         const double t = 2e-6 + (double)cdiv(units, cus) * 2.0 * 32 * 32 * (double)p.k / rate;
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
@@ -349,6 +357,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Pr
         return launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F64_64x128:
         return launch_mfma<double, 64, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
+    case F64_SMALL:
+        return launch_small(a, akc, bkc, nb, s);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);
@@ -372,8 +382,9 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
         for (int i = 0; i < nc; ++i) {
             if (!mfma_feasible(p, cands[i])) continue;
-            if (algo == SBX_ALGO_MFMA_TILE && cands[i] == F32_SMALL) continue;
-            if (algo == SBX_ALGO_MFMA_SMALL && cands[i] != F32_SMALL) continue;
+            const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL;
+            if (algo == SBX_ALGO_MFMA_TILE && small) continue;
+            if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
             const Choice c = model_plan(p, cands[i], cus);
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;

@@ -145,8 +145,10 @@ def test_huge_leading_dimension_falls_back_to_generic():
     # 2^22: 128-row tiles overflow, 64-row tiles still fit
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024).startswith(
         "mfma_f32_64x128")
-    # fp64 has no small kernel: 2^22 doubles per row is already too far for 64 rows
+    # fp64: 2^22 doubles per row is too far for 64 rows, not for 32
     assert sbx.gemm_select(1, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
+        "mfma_f64_32x32_ksplit4"
+    assert sbx.gemm_select(1, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \
         "generic_64x64x16"
 
 

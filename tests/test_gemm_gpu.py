@@ -153,8 +153,6 @@ SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (100, 37, 129), (257, 300, 45), (3
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_sweep_shapes_layouts_transposes(cuda, dtype, layout, ta, tb, algo):
-    if algo == 4 and dtype == np.float64:
-        pytest.skip("the small-problem kernel is fp32 only")
     for i, (m, n, k) in enumerate(SHAPES):
         alpha, beta = (1.0, 0.0) if i % 2 == 0 else (-0.75, 1.25)
         err, _, _ = _case(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, SEED + 10 + i,
@@ -202,8 +200,6 @@ def test_vector_loads_past_k_and_edges_ignore_padding(cuda, dtype, layout, ta, t
     straddles M or N feeds only C entries that are never stored.  Odd K,
     padded ld, bases off 16-byte alignment, every tile shape."""
     from gemm_cases import stored_dims
-    if algo == 4 and dtype == np.float64:
-        pytest.skip("the small-problem kernel is fp32 only")
     shapes = [(129, 67, 37), (300, 257, 301), (1001, 63, 303), (61, 1003, 305), (130, 67, 64)]
     if dtype == np.float32 and algo == 3:
         shapes.append((4095, 3001, 97))  # three-per-CU 128x128 tile
@@ -267,8 +263,6 @@ def test_empty_m_or_n_is_noop(cuda):
 def test_strided_batched(cuda, dtype, layout, algo):
     import torch
     import sushiblas_amd as sbx
-    if algo == 4 and dtype == np.float64:
-        pytest.skip("the small-problem kernel is fp32 only")
     batch, m, n, k = 5, 97, 130, 71
     ta, tb = 1, 0
     sa = (k, m) if ta else (m, k)
