@@ -112,8 +112,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
     } else {
         out[c++] = sq;
         if (f32) out[c++] = F32_128x128_O3;
-        out[c++] = m >= n ? tall : wide;
-        out[c++] = m >= n ? wide : tall;
+        // the two 64-wide tiles model alike; measured, 64x128 is the faster
+        // one on most square-ish shapes, so it comes first
+        out[c++] = wide;
+        out[c++] = tall;
     }
     out[c++] = f32 ? F32_SMALL : F64_SMALL;
     return c;

@@ -102,9 +102,9 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
 
 
 @pytest.mark.parametrize("m,n,k,expect", [
-    (1024, 1024, 1024, "mfma_f32_128x64x32_w2x2+splitk2"),     # under one round of 128x128
+    (1024, 1024, 1024, "mfma_f32_64x128x32_w2x2+splitk2"),     # under one round of 128x128
     (512, 1024, 1024, "mfma_f32_64x128x32_w2x2+splitk4"),
-    (2048, 2048, 2048, "mfma_f32_128x64x32_w2x2"),             # one full round of 512 slots
+    (2048, 2048, 2048, "mfma_f32_64x128x32_w2x2"),             # one full round of 512 slots
     (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
@@ -112,7 +112,7 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (4096, 4096, 1024, "mfma_f32_256x256x32_w2x2"),
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
-    (512, 512, 2048, "mfma_f32_128x64x32_w2x2+splitk8"),       # long K: the tile kernel's split
+    (512, 512, 2048, "mfma_f32_64x128x32_w2x2+splitk8"),       # long K: the tile kernel's split
 ])
 def test_model_based_selection(m, n, k, expect):
     """Tile shape and split from the cost model (whole rounds unsplit, the
