@@ -54,7 +54,8 @@ __device__ inline T finish(T acc, T alpha, T beta, const T* yp)
 
 // ---- rows: y[i] = alpha * A[i][:] . x + beta * y[i] -----------------------
 // grid.x: row groups of 256/LPR rows; grid.y: column chunks of `cw` columns.
-// VEC: A rows and x are 16-byte aligned and x is contiguous.
+// VEC: x is contiguous; A rows and x are read in 16-byte vectors whatever
+// their alignment (the device serves unaligned multi-dword loads).
 template <typename T, int LPR, bool VEC>
 __global__ void __launch_bounds__(256) gemv_rows_kernel(GemvArgs<T> p)
 {
@@ -112,8 +113,9 @@ __global__ void __launch_bounds__(256) gemv_rows_kernel(GemvArgs<T> p)
 
 // ---- cols: y[j] = alpha * sum_i A[i][j] x[i] + beta * y[j] -----------------
 // A workgroup: TC column threads x TR = 256/TC row threads; a column thread
-// owns VC consecutive columns (VC = V when A is 16-byte aligned row by row,
-// else 1).  grid.x: column strips of TC*VC; grid.y: row chunks of `cw` rows.
+// owns VC consecutive columns (V, read as one 16-byte vector at any row
+// alignment; 1 only through the plan's scalar form).  grid.x: column strips
+// of TC*VC; grid.y: row chunks of `cw` rows.
 template <typename T, int TC, int VC>
 __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
 {
@@ -125,13 +127,23 @@ __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
     T acc[VC];
 #pragma unroll
     for (int u = 0; u < VC; ++u) acc[u] = 0;
-    const bool whole = col + VC <= p.cols;  // all VC columns exist
     if (col < p.cols) {
         int64_t i = r0 + tr;
-        if (VC > 1 && whole) {
+        if (VC > 1) {
             typedef typename Vec16<T>::type vec_t;
+            // Whole vectors also for a strip's last, partial group of
+            // columns: the elements past the last column are padding or the
+            // next row's, and feed only accumulators that are never stored.
+            // Only rows whose vector ends inside the matrix take this path
+            // (for a partial group: all but the last one or two rows).
+            int64_t r_vec = r1;
+            if (col + VC > p.cols) {
+                const int64_t last = (p.rows - 1) * p.lda + p.cols - 1;  // last element
+                const int64_t room = last - (col + VC - 1);
+                r_vec = room < 0 ? 0 : min(r1, room / p.lda + 1);
+            }
             // four rows in flight per thread
-            for (; i + 3 * TR < r1; i += 4 * TR) {
+            for (; i + 3 * TR < r_vec; i += 4 * TR) {
                 vec_t av[4];
                 T xs[4];
 #pragma unroll
@@ -145,14 +157,16 @@ __global__ void __launch_bounds__(256) gemv_cols_kernel(GemvArgs<T> p)
 #pragma unroll
                     for (int e = 0; e < VC; ++e) acc[e] += av[u][e] * xs[u];
             }
-            for (; i < r1; i += TR) {
+            for (; i < r_vec; i += TR) {
                 const vec_t av =
                     __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(p.A + i * p.lda + col));
                 const T xs = p.x[i * p.incx];
 #pragma unroll
                 for (int e = 0; e < VC; ++e) acc[e] += av[e] * xs;
             }
-        } else {
+        }
+        {
+            // element loads: VC == 1, or the last rows of a partial group
             for (; i < r1; i += TR) {
                 const T xs = p.x[i * p.incx];
 #pragma unroll

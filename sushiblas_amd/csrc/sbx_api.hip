@@ -619,9 +619,10 @@ int gemv_run(hipStream_t stream, bool trans, int64_t rows, int64_t cols, T alpha
         return launch_scale<T>(y, incy, 0, ylen, 1, beta, 0, 0, 1, stream) == hipSuccess
                    ? SBX_OK : SBX_HIP_ERROR;
     }
-    constexpr int64_t V = 16 / (int64_t)sizeof(T);
-    const bool a_vec = (uintptr_t)A % 16 == 0 && lda % V == 0;
-    const bool vec = trans ? a_vec : (a_vec && incx == 1 && (uintptr_t)x % 16 == 0);
+    // 16-byte loads of A at any row alignment (the device serves unaligned
+    // multi-dword loads); the row-dot form also reads x in vectors, so it
+    // needs x contiguous
+    const bool vec = trans || incx == 1;
     GemvPlan pl = plan_gemv<T>(trans, rows, cols, vec, cu_count());
     GemvArgs<T> a;
     a.A = A; a.x = x; a.y = y;

@@ -50,11 +50,13 @@ def _err(got, want):
 # -- GEMV -------------------------------------------------------------------------
 
 def run_gemv(cuda, dtype, layout, trans, m, n, alpha, beta, seed, incx=1, incy=1, pad=0,
-             offsets=(0, 0, 0), y_init=None):
+             offsets=(0, 0, 0), y_init=None, nan_pad=False):
     import torch
     import sushiblas_amd as sbx
     lda = max(n if layout == 0 else m, 1) + pad
     A = oracle.fill_uniform(_alen(layout, m, n, lda), dtype, seed, 0)
+    if nan_pad:  # the ld padding must never be read
+        A[np.arange(A.size) % lda >= (n if layout == 0 else m)] = np.nan
     xlen, ylen = (m, n) if trans else (n, m)
     x = oracle.fill_uniform(max((xlen - 1) * incx + 1, 1), dtype, seed, 1)
     y = y_init.copy() if y_init is not None else \
@@ -87,7 +89,7 @@ def test_gemv_known_answer(cuda):
 
 # Shapes chosen to reach each kernel form: row-dot with 64/16/4 lanes per row,
 # with and without column chunks; column-axpy with 256..1 column threads, with
-# and without row chunks; vector and scalar loads.
+# and without row chunks.
 GEMV_CASES = [
     (4096, 4096), (257, 1023), (1, 100000), (100000, 1), (8192, 64), (64, 8192),
     (64, 262144), (131072, 16), (3, 5), (1000, 300), (2048, 2048),
@@ -107,8 +109,9 @@ def test_gemv_matches_oracle(cuda, dtype, layout, trans):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("trans", [0, 1])
 def test_gemv_strided_padded_unaligned(cuda, dtype, trans):
-    """incx/incy > 1, lda padding and base pointers off 16-byte alignment
-    (scalar-load kernel forms); entries between strided y elements untouched."""
+    """incx/incy > 1 (the row-dot form then reads x and A element by element),
+    lda padding and base pointers off 16-byte alignment; entries between
+    strided y elements untouched."""
     for m, n in ((300, 517), (5000, 70), (33, 20000)):
         for incx, incy, pad, off in ((2, 3, 3, (1, 1, 1)), (1, 1, 1, (0, 0, 0)),
                                      (1, 1, 0, (1, 0, 0)), (3, 1, 4, (0, 1, 0))):
@@ -118,6 +121,20 @@ def test_gemv_strided_padded_unaligned(cuda, dtype, trans):
             mask = np.ones(got.size, bool)
             mask[::incy] = False
             assert np.array_equal(got[mask], y0[mask])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("trans", [0, 1])
+def test_gemv_odd_ld_vector_loads(cuda, dtype, layout, trans):
+    """Odd leading dimensions and misaligned bases: A is still read in
+    16-byte vectors (at 4/8-byte aligned addresses); NaN in the ld padding
+    must not reach y."""
+    for m, n, pad in ((4095, 3001, 0), (1001, 777, 3), (33, 20001, 1), (20001, 33, 5), (7, 5, 1)):
+        got, want, _ = run_gemv(cuda, dtype, layout, trans, m, n, 0.5, 1.5, SEED + 70, pad=pad,
+                                offsets=(1, 0, 1), nan_pad=True)
+        assert np.isfinite(got).all(), (m, n)
+        assert _err(got, want) <= TOL[dtype], (m, n)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
