@@ -263,7 +263,7 @@ __device__ inline T relu_of(T x)
 //   X : tile extent along m (for A) or n (for B).
 //   KTAIL: K is not a multiple of VEC, so a k-contiguous vector may straddle K.
 // ---------------------------------------------------------------------------
-template <typename T, int X, int BK, bool KC, int PF, bool KTAIL>
+template <typename T, int X, int BK, bool KC, int PF, bool KTAIL, int NTHR = 256>
 struct Operand {
     static constexpr int V = 16 / (int)sizeof(T);
     static constexpr int VEC = V;  // elements per global load
@@ -272,43 +272,44 @@ struct Operand {
     static constexpr int ELEMS = KC ? X * LD : BK * LD;         // LDS tile size (elements)
     static constexpr int CONTIG = KC ? BK : X;                   // contiguous extent of tile
     static constexpr int VPR = CONTIG / VEC;                     // vectors per tile row
-    static constexpr int NV = X * BK / (VEC * 256);              // vectors per thread
-    static_assert(X * BK % (VEC * 256) == 0, "tile not divisible over 256 lanes");
+    static constexpr int NV = X * BK / (VEC * NTHR);             // vectors per thread
+    static_assert(X * BK % (VEC * NTHR) == 0, "tile not divisible over the lanes");
     typedef u32x4 raw_t;
 
-    int off[NV];       // byte offset of each vector relative to the tile base
-    int lds_off[NV];   // element offset in the LDS tile
-    int kidx[NV];      // k index of each vector within the tile
-    bool xok[NV];      // row/column validity along X (fixed for the block)
+    // Vector j of this thread is v = j*NTHR + tid of the tile, row
+    // r = j*RSTEP + r0, column c0 (NTHR is a multiple of VPR, so the column
+    // does not depend on j): only the j = 0 values are kept, the rest are
+    // affine in j (fewer live registers than one entry per vector).
+    static_assert(NTHR % VPR == 0, "rows per sweep must be whole");
+    static constexpr int RSTEP = NTHR / VPR;  // tile rows covered per j
+    int off0;          // byte offset of vector 0 relative to the tile base
+    int off_step;      // byte offset between vectors j and j + 1 (RSTEP rows)
+    int lds0;          // element offset of vector 0 in the LDS tile
+    int r0, c0;        // tile row and column of vector 0
+    int x_rem;         // rows/columns of the tile inside the matrix
     raw_t stage[PF][NV];  // register staging, PF tiles in flight
     int krem[PF];      // k extent left at the staged tile (k-tail masking)
 
-    __device__ inline void init(int tid, int64_t ld, int x_rem)
+    __device__ inline void init(int tid, int64_t ld, int x_rem_)
     {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            int v = j * 256 + tid;
-            int r = v / VPR;
-            int c = (v % VPR) * VEC;
-            off[j] = (int)((int64_t)r * ld + c) * (int)sizeof(T);
-            lds_off[j] = r * LD + c;
-            if (KC) {  // r: x index, c: k index
-                kidx[j] = c;
-                xok[j] = r < x_rem;
-            } else {   // r: k index, c: x index
-                kidx[j] = r;
-                xok[j] = c < x_rem;
-            }
-        }
+        r0 = tid / VPR;
+        c0 = (tid % VPR) * VEC;
+        off0 = (int)((int64_t)r0 * ld + c0) * (int)sizeof(T);
+        off_step = (int)((int64_t)RSTEP * ld) * (int)sizeof(T);
+        lds0 = r0 * LD + c0;
+        x_rem = x_rem_;
     }
+    // k index of vector j within the tile and whether its X index is inside
+    __device__ inline int kidx(int j) const { return KC ? c0 : r0 + j * RSTEP; }
+    __device__ inline bool xok(int j) const { return KC ? r0 + j * RSTEP < x_rem : c0 < x_rem; }
 
     template <int S>
     __device__ inline void load(__amdgpu_buffer_rsrc_t rs, int k_rem)
     {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            bool ok = xok[j] && kidx[j] < k_rem;
-            stage[S][j] = raw_load16(rs, ok ? off[j] : kOobOffset);
+            bool ok = xok(j) && kidx(j) < k_rem;
+            stage[S][j] = raw_load16(rs, ok ? off0 + j * off_step : kOobOffset);
         }
         krem[S] = k_rem;
     }
@@ -326,12 +327,12 @@ struct Operand {
         for (int j = 0; j < NV; ++j) {
             raw_t w = stage[S][j];
             if constexpr (KC && KTAIL) {
-                const int lim = krem[S] - kidx[j];  // elements of vector j inside K
+                const int lim = krem[S] - kidx(j);  // elements of vector j inside K
 #pragma unroll
                 for (int d = DPE; d < VEC * DPE; ++d)
                     w[d] = d / DPE < lim ? w[d] : 0u;
             }
-            *reinterpret_cast<raw_t*>(lds + lds_off[j]) = w;
+            *reinterpret_cast<raw_t*>(lds + lds0 + j * RSTEP * LD) = w;
         }
     }
 };
@@ -435,7 +436,7 @@ using Int = std::integral_constant<int, N>;
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
           bool KTAIL, int PF, int WPE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
     typedef Mfma<T> MF;
@@ -444,11 +445,12 @@ gemm_mfma_kernel(GemmArgs<T> p)
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int NBM = WTM / MB, NBN = WTN / MB;
     constexpr int G = BK / 8;  // k groups per tile
-    static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+    constexpr int NTHR = WAVES_M * WAVES_N * 64;
+    static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");
     static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
     static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
-    typedef Operand<T, BM, BK, A_KC, PF, KTAIL> OpA;
-    typedef Operand<T, BN, BK, B_KC, PF, KTAIL> OpB;
+    typedef Operand<T, BM, BK, A_KC, PF, KTAIL, NTHR> OpA;
+    typedef Operand<T, BN, BK, B_KC, PF, KTAIL, NTHR> OpB;
     typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
     typedef Frag<T, NBN, B_KC, OpB::LD> FragB;
 

@@ -42,7 +42,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 // (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp):
 // (T, BM, BN, BK, waves along M, waves along N, prefetch depth, waves/SIMD)
 #define SBX_MFMA_CONFIGS(X)  \
-    X(float, 256, 256, 32, 2, 2, 1, 1) \
+    X(float, 256, 256, 32, 4, 2, 1, 2) \
     X(float, 128, 128, 16, 2, 2, 2, 2) \
     X(float, 128, 128, 16, 2, 2, 2, 3) \
     X(float, 128, 64, 32, 2, 2, 2, 2) \

@@ -12,7 +12,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
 {
     const int tiles = a.tiles;
     const dim3 grid((unsigned)(a.num_full + (tiles - a.num_full) * a.split), 1, (unsigned)batch);
-    const dim3 block(256);
+    const dim3 block(WM * WN * 64);
     // k-tail masking is compiled in only where a k-contiguous operand meets a
     // K that is not a multiple of the 16-byte vector (it costs 1-4 %)
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
@@ -34,9 +34,10 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
     if (a.split > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        // the reduction runs 256 threads per block whatever the tile's waves
         constexpr int CHUNKS = BM * BN / 256;
         const dim3 rgrid((unsigned)((tiles - a.num_full) * CHUNKS), 1, (unsigned)batch);
-        splitk_reduce_kernel<T, BM, BN><<<rgrid, block, 0, stream>>>(a);
+        splitk_reduce_kernel<T, BM, BN><<<rgrid, dim3(256), 0, stream>>>(a);
     }
     return hipGetLastError();
 }

@@ -52,7 +52,7 @@ struct Problem {
 
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
 enum Cfg {
-    F32_256x256,   // large fp32: 4 waves of 128x128, 1 wave/SIMD (256 accumulators)
+    F32_256x256,   // large fp32: 8 waves of 64x128, 2 waves/SIMD (128 accumulators)
     F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
     F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
@@ -68,11 +68,11 @@ enum Cfg {
 struct CfgInfo {
     const char* name;
     int bm, bn, bk;
-    int per_cu;  // resident workgroups per CU (waves per SIMD of the config)
+    int per_cu;  // resident workgroups per CU
 };
 
 const CfgInfo kCfg[] = {
-    {"mfma_f32_256x256x32_w2x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
+    {"mfma_f32_256x256x32_w4x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
@@ -331,7 +331,7 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
 {
     switch (cfg) {
     case F32_256x256:
-        return launch_mfma<float, 256, 256, 32, 2, 2, 1, 1>(a, akc, bkc, nb, s);
+        return launch_mfma<float, 256, 256, 32, 4, 2, 1, 2>(a, akc, bkc, nb, s);
     case F32_128x128:
         return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_128x128_O3:

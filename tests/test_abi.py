@@ -83,7 +83,7 @@ def test_noop_cases_need_no_device():
 
 
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
-    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w2x2"),
+    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w4x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
     (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit4"),
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
@@ -109,7 +109,7 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
     (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
-    (4096, 4096, 1024, "mfma_f32_256x256x32_w2x2"),
+    (4096, 4096, 1024, "mfma_f32_256x256x32_w4x2"),
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
     (512, 512, 2048, "mfma_f32_64x128x32_w2x2+splitk8"),       # long K: the tile kernel's split
