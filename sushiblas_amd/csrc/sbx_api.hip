@@ -94,8 +94,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         int c = 0;
         const int64_t t = cdiv(n, 256);
         if (t * (t + 1) / 2 >= 256) out[c++] = F32_256x256;
-        out[c++] = F32_128x128;
+        // three per CU before two: timed on 8 triangles (1000..8192), the
+        // pick is then within 2.6 % of the fastest (8.2 % the other way)
         out[c++] = F32_128x128_O3;
+        out[c++] = F32_128x128;
         return c;
     }
     const bool f32 = dtype == SBX_F32;
@@ -109,6 +111,9 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         out[c++] = wide;
     } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 256) {
         out[c++] = F32_256x256;  // full rounds of the largest tile
+        // three 128^2 workgroups per CU beat it where the 256^2 grid ends
+        // in a ragged round or a ragged tile (5000^2 x 1000: 394 vs 450 us)
+        out[c++] = F32_128x128_O3;
     } else {
         out[c++] = sq;
         if (f32) out[c++] = F32_128x128_O3;
@@ -151,7 +156,8 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 // kernels on MI355X: every candidate tile x split of 24 fp32 and 24 fp64
 // shapes (512^3 .. 4096^3, the ragged 4095x3001x2047 in all four transposes,
 // K from 300 to 8192); the model's pick is on average within 0.7 % of the
-// fastest measured candidate, and at most 7 % off:
+// fastest measured candidate, and at most 7 % off (the same on 12 larger
+// fp32 shapes, 3072^3 .. 8192^2 x 4096, timed later):
 //   * a workgroup's work is w = 2*BM*BN*K_part / R, R = 0.55 TFLOP/s per CU
 //     (fp32; 0.275 fp64);
 //   * a config keeps P workgroups per CU (its waves per SIMD); a round of

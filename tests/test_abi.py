@@ -110,6 +110,8 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
     (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
     (4096, 4096, 1024, "mfma_f32_256x256x32_w4x2"),
+    (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2_o3+splitk3"),  # 400 ragged 256^2 tiles
+    (6144, 6144, 512, "mfma_f32_128x128x16_w2x2_o3"),           # 576 of 256^2: 2.25 rounds
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
     (512, 512, 2048, "mfma_f32_64x128x32_w2x2+splitk8"),       # long K: the tile kernel's split
@@ -122,8 +124,9 @@ def test_model_based_selection(m, n, k, expect):
 
 
 @pytest.mark.parametrize("dtype,n,k,expect", [
-    (0, 8192, 8192, "mfma_f32_128x128x16_w2x2+splitk6"),   # 2080 triangle tiles: 4 rounds + tail
-    (0, 5000, 5000, "mfma_f32_128x128x16_w2x2+splitk3"),
+    (0, 8192, 8192, "mfma_f32_128x128x16_w2x2_o3+splitk7"),  # 2080 triangle tiles
+    (0, 5000, 5000, "mfma_f32_128x128x16_w2x2_o3+splitk4"),
+    (0, 2048, 2048, "mfma_f32_128x128x16_w2x2_o3+splitk5"),
     (1, 8192, 8192, "mfma_f64_128x128x16_w2x2+splitk6"),
 ])
 def test_syrk_selection(dtype, n, k, expect):
