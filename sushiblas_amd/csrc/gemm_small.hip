@@ -160,21 +160,29 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
                         acc[bi][bj] = MF::mma(a[st].v[bi][s][kk], b[st].v[bj][s][kk], acc[bi][bj]);
     };
 
-    // two stages in flight; loads past the range are masked to zero, so the
-    // next stage is issued unconditionally (a wave with no k groups runs one
-    // all-zero stage)
+    // n stages of 32 k, two in flight (stage i in buffer i % 2).  Inside the
+    // loop the next stage is issued unconditionally; the last one or two
+    // stages are peeled so that nothing is loaded past the range (a load
+    // whose result is never used still delays the epilogue, which reuses
+    // its registers, by a full memory round trip)
     const int ke = 8 * g1;
     int k0 = 8 * g0;
-    issue(0, k0);
-    for (;;) {
+    const int n = (ke - k0 + 31) / 32;
+    if (n > 0) issue(0, k0);
+    int done = 0;  // stages consumed
+    for (; done + 2 < n; done += 2) {
         issue(1, k0 + 32);
         mma(0);
-        k0 += 32;
-        if (k0 >= ke) break;
-        issue(0, k0 + 32);
+        issue(0, k0 + 64);
         mma(1);
-        k0 += 32;
-        if (k0 >= ke) break;
+        k0 += 64;
+    }
+    if (n - done == 2) {
+        issue(1, k0 + 32);
+        mma(0);
+        mma(1);
+    } else if (n - done == 1) {
+        mma(0);
     }
 
     // partial tiles -> LDS, element (bi, bj, r, lane) at ((bi*NB + bj)*NACC + r)*64 + lane

@@ -170,11 +170,11 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     G + (partial bytes the reduction reads) / W with G = 7.5 us and
 //     W = 6 TB/s;
 //   * the one-launch small-problem kernel (32x32 tiles) takes
-//     2 us + ceil(tiles / CUs) * 2*32*32*K / Rs, Rs = 0.22 / 0.19 / 0.16
-//     TFLOP/s per CU with 2 / 1 / 0 k-contiguous operands, half that for
-//     fp64 (fitted on 28 more fp32 and 28 more fp64 shapes from 64^3 to
-//     2048x2048x256; with it the pick is within 0.9 % of the fastest on
-//     average over all 104 shapes).
+//     1 us + ceil(tiles / CUs) * 2*32*32*K / Rs, Rs = 0.2 TFLOP/s per CU
+//     for fp32 whatever the operand layout, 0.6 of that for fp64 (fitted
+//     on 26 more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256;
+//     with it the pick is within 0.6 % of the fastest on average over all
+//     108 shapes).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -222,22 +222,22 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
     return t;
 }
 
-// The fp64 small-problem kernel's rate relative to fp32's (fitted on 28
-// small fp64 shapes, 64^3 .. 2048x2048x256, with the tile kernels' splits
-// as the alternatives: the pick is within 0.9 % of the fastest on average)
-constexpr double kSmallF64Rate = 0.5;
+// The small-problem kernel's per-CU rate (fp32) and fp64's fraction of it,
+// fitted on 26 fp32 and 26 fp64 small shapes, 64^3 .. 2048x2048x256, with
+// the tile kernels' splits as the alternatives: over those and the 56
+// larger shapes the pick is within 0.6 % of the fastest on average
+constexpr double kSmallRate = 0.2e12;
+constexpr double kSmallF64Rate = 0.6;
 
 Choice model_plan(const Problem& p, Cfg c, int64_t cus)
 {
     if (c == F32_SMALL || c == F64_SMALL) {
         // one launch, no split: a CU works through its 32x32 tiles at a rate
-        // that hardly depends on how many share it (latency bound per wave);
-        // x-contiguous operands cost one element load per k step
-        const int kc = (p.ta ? 0 : 1) + (p.tb ? 1 : 0);
-        double rate = kc == 2 ? 0.22e12 : (kc == 1 ? 0.19e12 : 0.16e12);
-        if (c == F64_SMALL) rate *= kSmallF64Rate;
+        // that hardly depends on how many share it (latency bound per wave)
+        // or on the operands' layout
+        const double rate = c == F64_SMALL ? kSmallRate * kSmallF64Rate : kSmallRate;
         const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
-        const double t = 2e-6 + (double)cdiv(units, cus) * 2.0 * 32 * 32 * (double)p.k / rate;
+        const double t = 1e-6 + (double)cdiv(units, cus) * 2.0 * 32 * 32 * (double)p.k / rate;
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];
