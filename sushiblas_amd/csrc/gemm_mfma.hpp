@@ -6,10 +6,11 @@
 // which is the arithmetic the reference hands to oneMKL's
 // row_major::gemm / gemm_batch (src/ops/blas/level3/gemm.cpp:58,63).
 //
-// Design (one workgroup = 4 wave64s = 256 lanes, one macro tile BM x BN):
+// Design (one workgroup = WAVES_M x WAVES_N wave64s -- 4, or 8 for the
+// largest fp32 tile -- and one macro tile BM x BN):
 //  * Operands go global -> VGPR staging -> LDS -> VGPR fragments -> MFMA.
 //    Each operand keeps in LDS the layout it has in global memory, so every
-//    global read is a coalesced 16/8/4-byte buffer load along the contiguous
+//    global read is a coalesced 16-byte buffer load along the contiguous
 //    dimension and every LDS write is a straight vector store (no transposing
 //    scatter):
 //      "k-contiguous"  tile (A not transposed / B transposed): [X][BK + PAD]
