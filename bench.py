@@ -122,6 +122,18 @@ def read_traffic(workload):
     return None
 
 
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(A, B, C0, m, n, k, alpha, beta, got_full, target_s):
     """Oracle (port, fp32 accumulation) on the first R rows of the problem."""
     import numpy as np
@@ -149,7 +161,8 @@ def cpu_baseline(A, B, C0, m, n, k, alpha, beta, got_full, target_s):
     err_port = oracle.rel_fro_err(g, Cs.reshape(rows, n))
     base = {"value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"first {rows} of {m} rows of the same {m}x{n}x{k} fp32 GEMM "
-                      f"(oracle/sbo.c blocked OpenMP sgemm, fp32 accumulation, {dt:.1f} s)"}
+                      f"(oracle/sbo.c blocked OpenMP sgemm, fp32 accumulation, {dt:.1f} s)",
+            "cpu": cpu_model()}
     # The reference's CPU GEMM is oneMKL's sgemm (unbuildable here); torch's
     # CPU matmul is MKL sgemm, the same vendor family, so it is timed on the
     # same rows as a closer stand-in for that path.
