@@ -376,6 +376,27 @@ def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
         assert err <= TOL[np.float32], (m, n, k, name)
 
 
+# -- the largest fp32 tile on ragged edges ------------------------------------
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_largest_tile_ragged_edges(cuda, ta, tb):
+    """The 256x256 tile (8 waves) with partial tiles on both edges, a K tail
+    (257 = 8*32 + 1) and padded leading dimensions; 4097 x 8191 x 515 adds a
+    split tail.  The ldc padding of C stays untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k) in enumerate([(8191, 8190, 257), (4097, 8191, 515)]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 80 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"largest-tile case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name.startswith("mfma_f32_256x256"), name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 # -- split-K of under-filled grids ---------------------------------------------
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
