@@ -107,7 +107,11 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
     static_assert(PART == kTile * kTile, "a wave's blocks cover the tile once");
     __shared__ T red[4 * PART];  // the four waves' partial tiles
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    // uniform per wave, and known to be: the buffer descriptors built from
+    // it below stay scalar (as a vector value every load would need a loop
+    // over the distinct descriptors of the wave)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane % MB, q = lane / MB;
     const int tm = (int)(blockIdx.x % (unsigned)p.tiles_m);
     const int tn = (int)(blockIdx.x / (unsigned)p.tiles_m);

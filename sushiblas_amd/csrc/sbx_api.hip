@@ -169,12 +169,13 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //   * a split adds the reduction kernel and the partial round trip,
 //     G + (partial bytes the reduction reads) / W with G = 7.5 us and
 //     W = 6 TB/s;
-//   * the one-launch small-problem kernel (32x32 tiles) takes
-//     1 us + ceil(tiles / CUs) * 2*32*32*K / Rs, Rs = 0.2 TFLOP/s per CU
-//     for fp32 whatever the operand layout, 0.6 of that for fp64 (fitted
-//     on 26 more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256;
-//     with it the pick is within 0.6 % of the fastest on average over all
-//     108 shapes).
+//   * the one-launch small-problem kernel (32x32 tiles, work w = 2*32*32*K
+//     each) takes 2 us + max(ceil(tiles / 2CUs) * w / Rs, ceil(tiles /
+//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.35 TFLOP/s per CU for fp32
+//     whatever the operand layout, 0.7 of those for fp64 (fitted on 26
+//     more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256; with it
+//     the pick is within 0.6 % of the fastest on average over all 108
+//     shapes).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -222,22 +223,27 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
     return t;
 }
 
-// The small-problem kernel's per-CU rate (fp32) and fp64's fraction of it,
-// fitted on 26 fp32 and 26 fp64 small shapes, 64^3 .. 2048x2048x256, with
-// the tile kernels' splits as the alternatives: over those and the 56
-// larger shapes the pick is within 0.6 % of the fastest on average
-constexpr double kSmallRate = 0.2e12;
-constexpr double kSmallF64Rate = 0.6;
+// The small-problem kernel: a workgroup alone on a CU computes at
+// kSmallRate (it waits on its loads); a second one beside it costs nothing
+// extra, and past that the CU's kSmallCuRate limits.  fp64 runs at
+// kSmallF64Rate of the fp32 rates.  Fitted on 26 fp32 and 26 fp64 small
+// shapes, 64^3 .. 2048x2048x256, with the tile kernels' splits as the
+// alternatives: over those and the 56 larger shapes the pick is within
+// 0.6 % of the fastest on average.
+constexpr double kSmallRate = 0.21e12;
+constexpr double kSmallCuRate = 0.35e12;
+constexpr double kSmallF64Rate = 0.7;
 
 Choice model_plan(const Problem& p, Cfg c, int64_t cus)
 {
     if (c == F32_SMALL || c == F64_SMALL) {
-        // one launch, no split: a CU works through its 32x32 tiles at a rate
-        // that hardly depends on how many share it (latency bound per wave)
-        // or on the operands' layout
-        const double rate = c == F64_SMALL ? kSmallRate * kSmallF64Rate : kSmallRate;
+        // one launch, no split; the operands' layout hardly matters
+        const double f = c == F64_SMALL ? kSmallF64Rate : 1.0;
         const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
-        const double t = 1e-6 + (double)cdiv(units, cus) * 2.0 * 32 * 32 * (double)p.k / rate;
+        const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
+        const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
+        const double thr = (double)cdiv(units, cus) * w / (kSmallCuRate * f);
+        const double t = 2e-6 + (lat > thr ? lat : thr);
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];

@@ -102,8 +102,8 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
 
 
 @pytest.mark.parametrize("m,n,k,expect", [
-    (1024, 1024, 1024, "mfma_f32_64x128x32_w2x2+splitk2"),     # under one round of 128x128
-    (512, 1024, 1024, "mfma_f32_64x128x32_w2x2+splitk4"),
+    (1024, 1024, 1024, "mfma_f32_32x32_ksplit4"),              # 1024 32^2 tiles: 4 per CU
+    (512, 1024, 1024, "mfma_f32_32x32_ksplit4"),
     (2048, 2048, 2048, "mfma_f32_64x128x32_w2x2"),             # one full round of 512 slots
     (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
@@ -145,8 +145,9 @@ def test_huge_leading_dimension_falls_back_to_generic():
     # 2^23: only the 32-row tiles of the small-problem kernel still fit
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 23, 1024, 1024) == \
         "mfma_f32_32x32_ksplit4"
-    # 2^22: 128-row tiles overflow, 64-row tiles still fit
-    assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024).startswith(
+    # 2^22: 128-row tiles overflow, 64-row tiles still fit (2048^3: a shape
+    # the tile kernels win)
+    assert sbx.gemm_select(0, 0, 0, 0, 2048, 2048, 2048, 1 << 22, 2048, 2048).startswith(
         "mfma_f32_64x128")
     # fp64: 2^22 doubles per row is too far for 64 rows, not for 32
     assert sbx.gemm_select(1, 0, 0, 0, 1024, 1024, 1024, 1 << 22, 1024, 1024) == \
