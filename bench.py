@@ -13,6 +13,8 @@ Printed as one JSON line.  Besides the contract fields it carries:
                    rows of the same problem, on this host's cores
   parity        -- normwise error of the GPU result vs the oracle on the
                    sampled rows (identical input bits)
+  vendor        -- the same headline GEMM through torch.addmm (hipBLASLt)
+                   on the same device inputs, for context
   also          -- the other BASELINE configs timed the same way (fp64 8192^3,
                    the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), the
                    fused GEMM+ReLU epilogue against GEMM followed by ReLU, GEMV
@@ -21,7 +23,7 @@ Printed as one JSON line.  Besides the contract fields it carries:
                    patterns (microseconds per batch, one lane vs four)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
-                       [--cpu-seconds S] [--no-cpu]
+                       [--cpu-seconds S] [--no-cpu] [--no-vendor]
        python bench.py --only <also key>     (one secondary workload, for profiling)
        python bench.py --calibrate-copy      (1 GiB copy, the PMC byte reference)
 """
@@ -46,6 +48,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip timing the vendor library (torch.addmm) on the headline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -186,6 +190,28 @@ def cpu_baseline(A, B, C0, m, n, k, alpha, beta, got_full, target_s):
     parity = {"rows": rows, "normwise_vs_oracle_f64acc": err_truth,
               "normwise_vs_oracle_f32acc": err_port, "tolerance": 1e-5}
     return base, parity
+
+
+def vendor_headline(A, B, C, m, n, k, alpha, beta, steps, warmup):
+    """The same headline GEMM through torch.addmm (the vendor BLAS, hipBLASLt
+    on ROCm), fp32 with TF32 off, on the same device inputs, into a separate
+    output, timed the same way: context for the headline, not part of it."""
+    import torch
+    try:
+        torch.backends.cuda.matmul.allow_tf32 = False
+        A2, B2, C2 = A.view(m, k), B.view(k, n), C.view(m, n)
+        out = torch.empty_like(C2)
+
+        def step():
+            torch.addmm(C2, A2, B2, beta=beta, alpha=alpha, out=out)
+
+        ms = time_launches(step, steps, warmup, min_warm_s=0.25)
+        del out
+        torch.cuda.empty_cache()
+        return {"what": "torch.addmm (vendor BLAS) on the same inputs, fp32, TF32 off",
+                "ms": round(ms, 4), "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 3)}
+    except Exception as e:  # context only; never fails the bench
+        return {"error": str(e)[:200]}
 
 
 def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup, dist="uniform"):
@@ -421,6 +447,8 @@ def main():
     flops = 2.0 * m * n * k
     value = flops / (ms * 1e-3) / 1e12
     traffic = read_traffic("headline")
+    vendor = None if args.no_vendor else vendor_headline(A, B, C, m, n, k, alpha, beta,
+                                                         args.steps, args.warmup)
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -441,6 +469,8 @@ def main():
                      "unit": "TFLOP/s", "frac": round(value / PEAK["f32"], 4),
                      "traffic": traffic},
     }
+    if vendor is not None:
+        result["vendor"] = vendor
     if need_host:
         del A, B
         torch.cuda.empty_cache()
