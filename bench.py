@@ -14,7 +14,8 @@ Printed as one JSON line.  Besides the contract fields it carries:
   parity        -- normwise error of the GPU result vs the oracle on the
                    sampled rows (identical input bits)
   vendor        -- the same headline GEMM through torch.addmm (hipBLASLt)
-                   on the same device inputs, for context
+                   on the same device inputs, for context (and `vendor_ms`
+                   beside each GEMM config under `also`)
   also          -- the other BASELINE configs timed the same way (fp64 8192^3,
                    the ragged 4095x3001x2047 transposes, tall-skinny, 512^3), the
                    fused GEMM+ReLU epilogue against GEMM followed by ReLU, GEMV
@@ -49,7 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-vendor", action="store_true",
-                    help="skip timing the vendor library (torch.addmm) on the headline")
+                    help="skip timing the vendor library (torch.addmm) beside the GEMM configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -124,6 +125,9 @@ def read_traffic(workload):
             except ValueError:
                 return None
     return None
+
+
+VENDOR = True  # time torch (the vendor BLAS) beside each GEMM config; --no-vendor clears it
 
 
 def cpu_model():
@@ -251,6 +255,21 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
     out = {"kernel": name, "ms": round(ms, 4), "tflops": round(tflops, 3),
            "pct_peak": round(100 * tflops / PEAK[dtype], 2),
            "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    if VENDOR and layout == 0:
+        # the same problem through torch (the vendor BLAS) on the same
+        # device buffers, into a separate output, timed the same way
+        try:
+            opa = A.view(*sa).t() if ta else A.view(*sa)
+            opb = B.view(*sb).t() if tb else B.view(*sb)
+            c2, o2 = C.view(m, n), torch.empty(m, n, dtype=tdt, device="cuda")
+            torch.backends.cuda.matmul.allow_tf32 = False
+            vms = time_launches(lambda: torch.addmm(c2, opa, opb, beta=beta, alpha=alpha, out=o2),
+                                steps, warmup, min_warm_s=0.25)
+            out["vendor_ms"] = round(vms, 4)
+            del o2
+        except Exception as e:  # context only
+            out["vendor_ms"] = None
+            out["vendor_error"] = str(e)[:200]
     del A, B, C
     torch.cuda.empty_cache()
     return out
@@ -395,7 +414,9 @@ def secondary_workloads(steps_arg):
 
 
 def main():
+    global VENDOR
     args = parse()
+    VENDOR = not args.no_vendor
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
