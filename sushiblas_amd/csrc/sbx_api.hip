@@ -109,8 +109,8 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         out[c++] = tall;
     } else if (m <= 64) {
         out[c++] = wide;
-    } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 256) {
-        out[c++] = F32_256x256;  // full rounds of the largest tile
+    } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 192) {
+        out[c++] = F32_256x256;  // (nearly) full rounds of the largest tile
         // three 128^2 workgroups per CU beat it where the 256^2 grid ends
         // in a ragged round or a ragged tile (5000^2 x 1000: 394 vs 450 us)
         out[c++] = F32_128x128_O3;
@@ -170,12 +170,12 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     G + (partial bytes the reduction reads) / W with G = 7.5 us and
 //     W = 6 TB/s;
 //   * the one-launch small-problem kernel (32x32 tiles, work w = 2*32*32*K
-//     each) takes 2 us + max(ceil(tiles / 2CUs) * w / Rs, ceil(tiles /
-//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.35 TFLOP/s per CU for fp32
+//     each) takes 1.5 us + max(ceil(tiles / 2CUs) * w / Rs, ceil(tiles /
+//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.31 TFLOP/s per CU for fp32
 //     whatever the operand layout, 0.7 of those for fp64 (fitted on 26
-//     more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256; with it
-//     the pick is within 0.6 % of the fastest on average over all 108
-//     shapes).
+//     more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256 and 40
+//     random fp32 shapes from 300 to 7000 per dimension; over all 148
+//     shapes the pick is within 0.7 % of the fastest on average).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
@@ -227,11 +227,11 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
 // kSmallRate (it waits on its loads); a second one beside it costs nothing
 // extra, and past that the CU's kSmallCuRate limits.  fp64 runs at
 // kSmallF64Rate of the fp32 rates.  Fitted on 26 fp32 and 26 fp64 small
-// shapes, 64^3 .. 2048x2048x256, with the tile kernels' splits as the
-// alternatives: over those and the 56 larger shapes the pick is within
-// 0.6 % of the fastest on average.
+// shapes, 64^3 .. 2048x2048x256, and 40 random fp32 shapes, with the tile
+// kernels' splits as the alternatives: over those and the 56 larger shapes
+// the pick is within 0.7 % of the fastest on average.
 constexpr double kSmallRate = 0.21e12;
-constexpr double kSmallCuRate = 0.35e12;
+constexpr double kSmallCuRate = 0.31e12;
 constexpr double kSmallF64Rate = 0.7;
 
 Choice model_plan(const Problem& p, Cfg c, int64_t cus)
@@ -243,7 +243,7 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus)
         const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
         const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
         const double thr = (double)cdiv(units, cus) * w / (kSmallCuRate * f);
-        const double t = 2e-6 + (lat > thr ? lat : thr);
+        const double t = 1.5e-6 + (lat > thr ? lat : thr);
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];
