@@ -98,14 +98,14 @@ struct SmallOperand {
     }
 };
 
-template <typename T, bool A_KC, bool B_KC, bool KTAIL>
-__global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
+template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL>
+__global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
 {
     typedef Mfma<T> MF;
     constexpr int MB = MF::MB, V = MF::V, NB = kTile / MB, NACC = MF::NACC;
     constexpr int PART = NB * NB * NACC * 64;  // one wave's partial tile
     static_assert(PART == kTile * kTile, "a wave's blocks cover the tile once");
-    __shared__ T red[4 * PART];  // the four waves' partial tiles
+    __shared__ T red[NW * PART];  // the waves' partial tiles
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // uniform per wave, and known to be: the buffer descriptors built from
@@ -123,8 +123,8 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
 
     // this wave's k groups [g0, g1) of the ceil(K/8); k past k_lim is zeroed
     const int ng = (p.K + 7) / 8;
-    const int g0 = (int)((int64_t)wave * ng / 4);
-    const int g1 = (int)((int64_t)(wave + 1) * ng / 4);
+    const int g0 = (int)((int64_t)wave * ng / NW);
+    const int g1 = (int)((int64_t)(wave + 1) * ng / NW);
     const int k_lim = min(p.K, 8 * g1);
 
     // operand origin (tile, k = 0) and the elements from there to the matrix end
@@ -199,13 +199,16 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
                 red[wave * PART + ((bi * NB + bj) * NACC + r) * 64 + lane] = acc[bi][bj][r];
     __syncthreads();
 
-    // each lane finishes 4 elements of the 32x32 tile
+    // each lane finishes 1024 / (64 NW) elements of the 32x32 tile, summing
+    // the waves' partials in wave order
     const T alpha = p.alpha, beta = p.beta;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int e = u * 256 + tid;
+    for (int u = 0; u < kTile * kTile / (NW * 64); ++u) {
+        const int e = u * (NW * 64) + tid;
         const int el = e & 63, r = (e >> 6) % NACC, blk = (e >> 6) / NACC;
-        const T sum = ((red[e] + red[PART + e]) + red[2 * PART + e]) + red[3 * PART + e];
+        T sum = red[e];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += red[w * PART + e];
         const int row = (blk / NB) * MB + MF::row(r, el / MB), col = (blk % NB) * MB + el % MB;
         const int m = m0 + row, n = n0 + col;
         if (m < p.M && n < p.N) {
@@ -219,13 +222,16 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(GemmArgs<T> p)
 
 }  // namespace
 
-template <typename T>
-hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream)
+namespace {
+template <typename T, int NW>
+hipError_t launch_small_nw(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch,
+                           hipStream_t stream)
 {
     const dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)batch);
-    const dim3 block(256);
+    const dim3 block(NW * 64);
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
-#define SBX_LAUNCH(AK, BKC, TAIL) gemm_small_kernel<T, AK, BKC, TAIL><<<grid, block, 0, stream>>>(a)
+#define SBX_LAUNCH(AK, BKC, TAIL) \
+    gemm_small_kernel<T, NW, AK, BKC, TAIL><<<grid, block, 0, stream>>>(a)
     if (a_kc && b_kc) {
         if (tail) SBX_LAUNCH(true, true, true);
         else SBX_LAUNCH(true, true, false);
@@ -241,8 +247,18 @@ hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, h
 #undef SBX_LAUNCH
     return hipGetLastError();
 }
+}  // namespace
 
-template hipError_t launch_small<float>(const GemmArgs<float>&, bool, bool, int, hipStream_t);
-template hipError_t launch_small<double>(const GemmArgs<double>&, bool, bool, int, hipStream_t);
+template <typename T>
+hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream,
+                        int waves)
+{
+    if (waves == 8) return launch_small_nw<T, 8>(a, a_kc, b_kc, batch, stream);
+    return launch_small_nw<T, 4>(a, a_kc, b_kc, batch, stream);
+}
+
+template hipError_t launch_small<float>(const GemmArgs<float>&, bool, bool, int, hipStream_t, int);
+template hipError_t launch_small<double>(const GemmArgs<double>&, bool, bool, int, hipStream_t,
+                                         int);
 
 }  // namespace sbx

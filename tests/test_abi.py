@@ -85,7 +85,7 @@ def test_noop_cases_need_no_device():
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w4x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
-    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit4"),
+    (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit8"),  # one tile per CU, K >= 512
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
     (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_32x32_ksplit4"),
     (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
@@ -113,6 +113,7 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2_o3+splitk3"),  # 400 ragged 256^2 tiles
     (6144, 6144, 512, "mfma_f32_128x128x16_w2x2_o3"),           # 576 of 256^2: 2.25 rounds
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
+    (128, 1024, 512, "mfma_f32_32x32_ksplit8"),                # 128 tiles, K = 512: 8 waves
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
     (512, 512, 2048, "mfma_f32_64x128x32_w2x2+splitk8"),       # long K: the tile kernel's split
 ])

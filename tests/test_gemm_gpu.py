@@ -376,6 +376,28 @@ def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
         assert err <= TOL[np.float32], (m, n, k, name)
 
 
+# -- the small-problem kernel with K cut over 8 waves ---------------------------
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_small_kernel_eight_waves(cuda, ta, tb):
+    """At most one 32x32 tile per CU and K >= 512 select the 8-wave form:
+    512^3, and a ragged 300 x 200 x 1001 with padded leading dimensions and
+    misaligned bases (K tail, partial tiles); C outside the window untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k, pad, off) in enumerate([(512, 512, 512, (0, 0, 0), (0, 0, 0)),
+                                             (300, 200, 1001, (3, 1, 5), (1, 2, 3))]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i, pad)
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"eight-wave case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == "mfma_f32_32x32_ksplit8", name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc,
+                      offsets=off)
+        want = run_oracle(0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 # -- the largest fp32 tile on ragged edges ------------------------------------
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
