@@ -47,6 +47,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
     X(float, 128, 128, 16, 2, 2, 2, 2) \
     X(float, 128, 128, 16, 2, 2, 2, 3) \
     X(float, 128, 64, 32, 2, 2, 2, 2) \
+    X(float, 256, 64, 32, 8, 1, 2, 2) \
     X(float, 64, 128, 32, 2, 2, 2, 2) \
     X(double, 128, 128, 16, 2, 2, 1, 2) \
     X(double, 128, 64, 16, 2, 2, 2, 2) \

@@ -56,6 +56,7 @@ enum Cfg {
     F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
     F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
+    F32_256x64,    // n <= 64 with a full round of 256-row tiles: 8 waves of 32x64
     F32_64x128,    // m <= 64
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
@@ -75,7 +76,8 @@ struct CfgInfo {
 const CfgInfo kCfg[] = {
     {"mfma_f32_256x256x32_w4x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
-    {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
+    {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
+    {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
     {"mfma_f64_32x32_ksplit4", 32, 32, 32, 1},     {"mfma_f32_32x32_ksplit8", 32, 32, 32, 1},
@@ -108,6 +110,9 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
     const Cfg wide = f32 ? F32_64x128 : F64_64x128;   // m <= 64
     int c = 0;
     if (n <= 64) {
+        // one 8-wave 256-row workgroup per CU: B is read by half as many
+        // workgroups (65536 x 64 x 4096: 291-294 us against 296-300)
+        if (f32 && cdiv(m, 256) >= 256) out[c++] = F32_256x64;
         out[c++] = tall;
     } else if (m <= 64) {
         out[c++] = wide;
@@ -352,6 +357,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 128, 128, 16, 2, 2, 2, 3>(a, akc, bkc, nb, s);
     case F32_128x64:
         return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
+    case F32_256x64:
+        return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2>(a, akc, bkc, nb, s);
     case F32_64x128:
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_SMALL:

@@ -86,9 +86,9 @@ def test_noop_cases_need_no_device():
     (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w4x2"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
     (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit8"),  # one tile per CU, K >= 512
-    (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_128x64x32_w2x2"),
+    (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_256x64x32_w8x1"),
     (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_32x32_ksplit4"),
-    (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_128x64x32_w2x2"),
+    (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_256x64x32_w8x1"),
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
 ])

@@ -419,6 +419,26 @@ def test_largest_tile_ragged_edges(cuda, ta, tb):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_tall_skinny_eight_wave_tile(cuda, ta, tb):
+    """The 8-wave 256x64 tile (n <= 64 with a full round of 256-row tiles):
+    a ragged last row tile, n = 63, a K tail (515 = 16*32 + 3) and padded
+    leading dimensions; 65536 x 64 x 1000 is a whole round with a K tail.  The
+    ldc padding of C stays untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k) in enumerate([(65535, 63, 515), (65536, 64, 1000)]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name.startswith("mfma_f32_256x64x32_w8x1"), name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 # -- split-K of under-filled grids ---------------------------------------------
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
