@@ -449,7 +449,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     constexpr int NTHR = WAVES_M * WAVES_N * 64;
     static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");
     static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
-    static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
+    static_assert(PF >= 1 && PF <= 4, "prefetch depth 1 to 4");
     typedef Operand<T, BM, BK, A_KC, PF, KTAIL, NTHR> OpA;
     typedef Operand<T, BN, BK, B_KC, PF, KTAIL, NTHR> OpB;
     typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
@@ -551,21 +551,23 @@ gemm_mfma_kernel(GemmArgs<T> p)
     constexpr int NLD = OpA::NV + OpB::NV;  // global loads (= LDS writes) per tile
     static_assert(G % 2 == 0, "fragment double-buffering needs an even number of k groups");
 
-    // One k tile held in LDS buffer cur (= kt & 1), its group-0 fragments
-    // already in registers.  Region A: the MFMAs of groups 0..G-2 overlap the
-    // next tile's global loads, the fragment reads of groups 1..G-1 and the
-    // LDS writes of the next tile.  Then one barrier.  Region B: the MFMAs of
-    // the last group overlap the fragment reads of the next tile's group 0.
-    // With PF == 2, staging set S holds tile kt + 1 on entry and set S ^ 1
-    // receives tile kt + 2, so the LDS writes never wait on fresh loads.
+    // One k tile held in LDS buffer cur, its group-0 fragments already in
+    // registers.  Region A: the MFMAs of groups 0..G-2 overlap the global
+    // loads of tile kt + PF, the fragment reads of groups 1..G-1 and the LDS
+    // writes of tile kt + 1.  Then one barrier.  Region B: the MFMAs of the
+    // last group overlap the fragment reads of the next tile's group 0.
+    // Tile t is staged in register set (t - kt0) % PF, so step S (= (kt -
+    // kt0) % PF) loads into set S -- free since tile kt went to LDS -- and
+    // stores set (S + 1) % PF, which holds tile kt + 1 (with PF == 1, the
+    // tile this step loads).  PF tiles are in flight, so the LDS writes wait
+    // on loads issued PF - 1 steps earlier.
     // The loads, LDS writes and next-tile reads are issued unconditionally so
     // that each region is one basic block the scheduling hints can interleave:
     // past the last k tile the buffer loads are masked (k_rem <= 0 or the
     // next part's data) and what they write to the idle LDS buffer is unused.
     auto step = [&](auto S, int kt, int cur) {
         constexpr int st = decltype(S)::value;
-        if constexpr (PF == 1) issue(Int<0>{}, kt + 1);
-        else issue(Int<st ^ 1>{}, kt + 2);
+        issue(Int<st>{}, kt + PF);
 #pragma unroll
         for (int g = 0; g + 1 < G; ++g) {
             if (((g + 1) & 1) == 0) read_frags(Int<0>{}, cur, g + 1);
@@ -573,7 +575,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
             if ((g & 1) == 0) mma(Int<0>{});
             else mma(Int<1>{});
         }
-        commit(Int<PF == 1 ? 0 : st>{}, cur ^ 1);
+        commit(Int<(st + 1) % PF>{}, cur ^ 1);
         // region A: loads first, then fragment reads, then the LDS writes,
         // each memory instruction followed by a slice of the MFMAs
         {
@@ -612,24 +614,29 @@ gemm_mfma_kernel(GemmArgs<T> p)
         }
     };
 
-    // prologue: tile kt0 -> LDS buffer 0 (and tile kt0+1 -> staging set 0 if PF == 2)
-    if constexpr (PF == 1) {
-        issue(Int<0>{}, kt0);
-        commit(Int<0>{}, 0);
-    } else {
-        issue(Int<PF - 1>{}, kt0);
-        commit(Int<PF - 1>{}, 0);
-        issue(Int<0>{}, kt0 + 1);
-    }
+    // prologue: tile kt0 -> set 0 -> LDS buffer 0; tiles kt0+1 .. kt0+PF-1
+    // -> sets 1 .. PF-1
+    issue(Int<0>{}, kt0);
+    commit(Int<0>{}, 0);
+    if constexpr (PF > 1) issue(Int<1>{}, kt0 + 1);
+    if constexpr (PF > 2) issue(Int<2>{}, kt0 + 2);
+    if constexpr (PF > 3) issue(Int<3>{}, kt0 + 3);
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
 
     if constexpr (PF == 1) {
         for (int kt = kt0; kt < nk; ++kt) step(Int<0>{}, kt, (kt - kt0) & 1);
     } else {
-        for (int kt = kt0; kt < nk; kt += 2) {
-            step(Int<0>{}, kt, 0);
-            if (kt + 1 < nk) step(Int<1>{}, kt + 1, 1);
+        for (int kt = kt0; kt < nk; kt += PF) {
+            const int cur = (kt - kt0) & 1;
+            step(Int<0>{}, kt, cur);
+            if (kt + 1 < nk) step(Int<1 % PF>{}, kt + 1, cur ^ 1);
+            if constexpr (PF > 2) {
+                if (kt + 2 < nk) step(Int<2 % PF>{}, kt + 2, cur);
+            }
+            if constexpr (PF > 3) {
+                if (kt + 3 < nk) step(Int<3 % PF>{}, kt + 3, cur ^ 1);
+            }
         }
     }
 

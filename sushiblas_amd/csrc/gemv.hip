@@ -33,15 +33,19 @@ namespace sbx {
 
 namespace {
 
+// 16-byte vectors whose alignment is only the element's: A's rows and x may
+// start at any element, so a vector load is well-defined C++ at 4-byte (fp32)
+// or 8-byte (fp64) aligned addresses.  gfx950 serves such loads with one
+// 16-byte instruction (the device runs in unaligned access mode).
 template <typename T>
 struct Vec16;
 template <>
 struct Vec16<float> {
-    typedef float type __attribute__((ext_vector_type(4)));
+    typedef float type __attribute__((ext_vector_type(4), aligned(4)));
 };
 template <>
 struct Vec16<double> {
-    typedef double type __attribute__((ext_vector_type(2)));
+    typedef double type __attribute__((ext_vector_type(2), aligned(8)));
 };
 
 template <typename T>

@@ -9,9 +9,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/sbx.h"
 #include "gemv.hpp"
@@ -189,7 +191,7 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 // Split partials live in a workspace cached per (device, stream): calls on
 // one stream are ordered, so they can share it; the first call that needs
 // more memory grows it (the only allocation on the GEMM path; outgrown
-// buffers are kept, see stream_workspace).  The reduction sums the parts in
+// buffers are kept, see WorkspaceLease).  The reduction sums the parts in
 // fixed order, so results are deterministic.
 // ---------------------------------------------------------------------------
 constexpr int kMaxSplit = kMaxSplitParts;
@@ -297,53 +299,134 @@ int cu_count()
     return g_cu_count[dev];
 }
 
+// Split-K partials and chunked-GEMV partials live in a workspace keyed by
+// (device, stream): calls on one stream run in order, so they can share it.
+// hipStreamPerThread names a different stream in every host thread, so for
+// that handle the key is the calling thread instead (a thread number that is
+// never reused), and a thread's workspaces go to a per-device pool when the
+// thread exits.  Every use is ordered after the previous one through an
+// event: the stream waits on the event recorded after the workspace's last
+// use before its kernels are enqueued, so a workspace that passes to another
+// stream -- a pooled one, or a stream handle that the runtime hands out again
+// after hipStreamDestroy -- is never written while older kernels may still
+// read it.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
+    hipEvent_t last = nullptr;  // recorded after the latest use
     // Held from handing out the workspace until the calls that use it are
     // enqueued: a split GEMM (or chunked GEMV) is two kernels, and another
     // host thread's call on the same stream must not land between them and
     // overwrite the partials the second kernel is about to read.
     std::mutex launch_mu;
 };
-std::mutex g_ws_mutex;
-// never destroyed: freeing device memory during process teardown is unsafe
-std::map<std::pair<int, hipStream_t>, Workspace>* g_ws =
-    new std::map<std::pair<int, hipStream_t>, Workspace>();
 
-// A stream's workspace with its launch lock held.
-struct WorkspaceLease {
-    void* ptr = nullptr;
-    std::unique_lock<std::mutex> lock;
+struct WsKey {
+    int dev;
+    hipStream_t stream;
+    uint64_t thread;  // calling thread for hipStreamPerThread, else 0
+    bool operator<(const WsKey& o) const
+    {
+        if (dev != o.dev) return dev < o.dev;
+        if (stream != o.stream) return stream < o.stream;
+        return thread < o.thread;
+    }
 };
 
-// A workspace of at least `bytes` for `stream` (ptr null if it cannot be
-// allocated), locked for the caller's launches.  A workspace that is outgrown
-// is retired, not freed: kernels enqueued earlier on the stream may not have
-// run yet.  Growth at least doubles, so the retired buffers add up to less
-// than the live one.
-WorkspaceLease stream_workspace(hipStream_t stream, size_t bytes)
-{
-    WorkspaceLease lease;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return lease;
-    Workspace* w;
+std::mutex g_ws_mutex;
+// never destroyed: freeing device memory during process teardown is unsafe
+std::map<WsKey, Workspace*>* g_ws = new std::map<WsKey, Workspace*>();
+std::map<int, std::vector<Workspace*>>* g_ws_pool = new std::map<int, std::vector<Workspace*>>();
+std::atomic<uint64_t> g_next_thread{1};
+
+// The calling thread's number, and on thread exit the return of the
+// workspaces it keyed through hipStreamPerThread to the pool.  Pooled
+// workspaces keep their buffers and events; their next user waits on the
+// event, which covers work the exited thread left in flight.
+struct ThreadWorkspaces {
+    uint64_t id = g_next_thread.fetch_add(1);
+    std::vector<WsKey> keys;
+    ~ThreadWorkspaces()
     {
         std::lock_guard<std::mutex> g(g_ws_mutex);
-        w = &(*g_ws)[{dev, stream}];  // map nodes never move
+        for (const WsKey& k : keys) {
+            auto it = g_ws->find(k);
+            if (it == g_ws->end()) continue;
+            (*g_ws_pool)[k.dev].push_back(it->second);
+            g_ws->erase(it);
+        }
     }
-    lease.lock = std::unique_lock<std::mutex>(w->launch_mu);
-    if (w->bytes < bytes) {
-        size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
-        if (nb < 2 * w->bytes) nb = 2 * w->bytes;
-        void* p = nullptr;
-        if (hipMalloc(&p, nb) != hipSuccess) return lease;  // ptr null; the old one stays
-        w->base = p;
-        w->bytes = nb;
+};
+thread_local ThreadWorkspaces t_ws;
+
+// A workspace of at least `bytes` for the calling thread's `stream`, locked
+// for the caller's launches until release (ptr null if it cannot be
+// allocated).  A workspace that is outgrown is retired, not freed: kernels
+// enqueued earlier may not have run yet.  Growth at least doubles, so the
+// retired buffers add up to less than the live one.
+struct WorkspaceLease {
+    void* ptr = nullptr;
+    Workspace* w = nullptr;
+    hipStream_t stream = nullptr;
+    std::unique_lock<std::mutex> lock;
+
+    bool acquire(hipStream_t s, size_t bytes)
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return false;
+        const bool per_thread = s == hipStreamPerThread;
+        const WsKey key{dev, s, per_thread ? t_ws.id : 0};
+        Workspace* ws;
+        {
+            std::lock_guard<std::mutex> g(g_ws_mutex);
+            auto it = g_ws->find(key);
+            if (it != g_ws->end()) {
+                ws = it->second;
+            } else {
+                std::vector<Workspace*>& pool = (*g_ws_pool)[dev];
+                if (!pool.empty()) {
+                    ws = pool.back();
+                    pool.pop_back();
+                } else {
+                    ws = new Workspace();
+                }
+                (*g_ws)[key] = ws;
+                if (per_thread) t_ws.keys.push_back(key);
+            }
+        }
+        lock = std::unique_lock<std::mutex>(ws->launch_mu);
+        if (!ws->last && hipEventCreateWithFlags(&ws->last, hipEventDisableTiming) != hipSuccess) {
+            ws->last = nullptr;
+            return false;
+        }
+        if (ws->bytes < bytes) {
+            size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
+            if (nb < 2 * ws->bytes) nb = 2 * ws->bytes;
+            void* p = nullptr;
+            if (hipMalloc(&p, nb) != hipSuccess) return false;  // the old buffer stays
+            ws->base = p;
+            ws->bytes = nb;
+        }
+        // order this use after the previous one, whichever stream made it
+        if (hipStreamWaitEvent(s, ws->last, 0) != hipSuccess) return false;
+        w = ws;
+        stream = s;
+        ptr = ws->base;
+        return true;
     }
-    lease.ptr = w->base;
-    return lease;
-}
+
+    // Record the end of this use (after the caller's launches), then let the
+    // next caller in.
+    hipError_t release()
+    {
+        hipError_t e = hipSuccess;
+        if (w) e = hipEventRecord(w->last, stream);
+        w = nullptr;
+        if (lock.owns_lock()) lock.unlock();
+        return e;
+    }
+    ~WorkspaceLease() { (void)release(); }
+};
 
 hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Problem& p,
                       int nb, hipStream_t s)
@@ -436,9 +519,10 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     void* ws = nullptr;
     WorkspaceLease lease;  // held until both split kernels are enqueued
     if (sp.split > 1) {
-        lease = stream_workspace(stream, (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T));
-        ws = lease.ptr;
-        if (!ws) sp = SplitPlan{(int)tiles, 1, 0};  // no memory: run unsplit
+        if (lease.acquire(stream, (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T)))
+            ws = lease.ptr;
+        else
+            sp = SplitPlan{(int)tiles, 1, 0};  // no memory: run unsplit
     }
 
     for (int64_t b0 = 0; b0 < p.batch; b0 += kMaxGridZ) {
@@ -475,7 +559,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         }
         if (e != hipSuccess) return SBX_HIP_ERROR;
     }
-    return SBX_OK;
+    return lease.release() == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
 }
 
 int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
@@ -663,14 +747,15 @@ int gemv_run(hipStream_t stream, bool trans, int64_t rows, int64_t cols, T alpha
     a.ws = nullptr;
     WorkspaceLease lease;  // held until the partial and finish kernels are enqueued
     if (pl.chunks > 1) {
-        lease = stream_workspace(stream, (size_t)pl.chunks * pl.out_len * sizeof(T));
-        a.ws = (T*)lease.ptr;
+        a.ws = lease.acquire(stream, (size_t)pl.chunks * pl.out_len * sizeof(T))
+                   ? (T*)lease.ptr : nullptr;
         if (!a.ws) {  // no memory for partials: one range
             pl.chunks = 1;
             pl.cw = trans ? rows : cols;
         }
     }
-    return launch_gemv<T>(a, pl, stream) == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
+    if (launch_gemv<T>(a, pl, stream) != hipSuccess) return SBX_HIP_ERROR;
+    return lease.release() == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
 }
 
 int gemv_impl(void* stream, int dtype, int layout, int trans, int64_t m, int64_t n,

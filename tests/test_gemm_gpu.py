@@ -502,6 +502,58 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
             assert normwise(0, o.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32]
 
 
+HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread: a different stream in every host thread
+
+
+def test_split_k_per_thread_streams(cuda):
+    """hipStreamPerThread names one stream per host thread, so two threads
+    issuing split-K GEMMs through it run concurrently on different streams:
+    each thread must get its own workspace.  A third and fourth thread start
+    after the first two have exited, without any synchronization, and take
+    their pooled workspaces (the event recorded after the last use orders
+    them after the exited threads' kernels).  Every result must match the
+    oracle."""
+    import threading
+    import torch
+    import sushiblas_amd as sbx
+    shapes = [(512, 512, 2048), (384, 320, 3000)]
+    data = []
+    for i, (m, n, k) in enumerate(shapes):
+        name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+        assert "+splitk" in name, name
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 73 + i)
+        want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+        data.append((m, n, k, torch.from_numpy(A).to(cuda), lda, torch.from_numpy(B).to(cuda),
+                     ldb, ldc, want))
+    outs = {t: [[torch.zeros(d[0] * d[1], device=cuda) for _ in range(4)] for d in data]
+            for t in range(4)}
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        try:
+            for rep in range(4):
+                for j in ((t + rep) % 2, (t + rep + 1) % 2):
+                    m, n, k, dA, lda, dB, ldb, ldc, _ = data[j]
+                    sbx.sgemm(0, 0, 0, m, n, k, 1.0, dA, lda, dB, ldb, 0.0, outs[t][j][rep], ldc,
+                              stream=HIP_STREAM_PER_THREAD)
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    for wave in ((0, 1), (2, 3)):
+        threads = [threading.Thread(target=worker, args=(t,)) for t in wave]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+    torch.cuda.synchronize()  # waits for every stream, the per-thread ones included
+    assert not errors, errors
+    for t in range(4):
+        for (m, n, k, _, _, _, _, ldc, want), group in zip(data, outs[t]):
+            for o in group:
+                assert normwise(0, o.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32], (t, m)
+
+
 def test_split_k_on_two_streams(cuda):
     """Each stream has its own split-K workspace: concurrent calls on two
     streams do not corrupt each other."""
