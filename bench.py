@@ -11,8 +11,10 @@ Printed as one JSON line.  Besides the contract fields it carries:
   cpu_baseline  -- the CPU oracle (oracle/, a port: the reference's oneMKL
                    SYCL path cannot be built here) timed on a bounded sample of
                    rows of the same problem, on this host's cores
-  parity        -- normwise error of the GPU result vs the oracle on the
-                   sampled rows (identical input bits)
+  parity        -- normwise error of the GPU result vs the oracle
+                   (accumulating in double) over the whole matrix, on
+                   identical input bits; each BASELINE GEMM config under
+                   `also` carries its own cpu_baseline and parity too
   vendor        -- the same headline GEMM through torch.addmm (hipBLASLt)
                    on the same device inputs, for context (and `vendor_ms`
                    beside each GEMM config under `also`)
@@ -142,57 +144,82 @@ def cpu_model():
     return None
 
 
-def cpu_baseline(A, B, C0, m, n, k, alpha, beta, got_full, target_s):
-    """Oracle (port, fp32 accumulation) on the first R rows of the problem."""
+def _host_view(X, trans, rows, cols, ld):
+    """op(X) (rows x cols) of a flat row-major buffer with leading dimension
+    ld, as a 2-D numpy view: the stored matrix itself when not transposed,
+    else the transpose of the stored cols x rows matrix.  The buffer must
+    hold whole rows of ld elements (bench.py allocates exactly that)."""
+    sr, sc = (cols, rows) if trans else (rows, cols)
+    stored = X[:sr * ld].reshape(sr, ld)[:, :sc]
+    return stored.T if trans else stored
+
+
+def cpu_leg(dtype, ta, tb, m, n, k, alpha, beta, A, lda, B, ldb, C0, ldc, got, target_s):
+    """CPU baseline and parity for one row-major GEMM configuration.
+
+    cpu_baseline: the oracle (oracle/sbo.c, a port: the reference's oneMKL SYCL
+    path cannot be built here) timed on the first R rows of op(A) / C, R sized
+    for about target_s seconds and capped at m; beside it MKL through torch's
+    CPU addmm on the same rows (BLAS_INFO=mkl: the vendor family of the
+    reference's oneMKL CPU gemm, src/ops/blas/level3/gemm.cpp:63).
+    parity: the GPU result over the WHOLE m x n matrix against the oracle
+    accumulating in double on identical input bits (normwise relative
+    Frobenius error), and the same for the timed port's rows."""
     import numpy as np
     import oracle
     threads = oracle.num_threads()
-    # calibrate on 64 rows, then size the sample to ~target_s seconds
-    r0 = 64
-    Cs = np.array(C0[:r0 * n], copy=True)
-    t = time.perf_counter()
-    oracle.gemm(0, 0, 0, r0, n, k, alpha, np.array(A[:r0 * k], copy=True), k, B, n, beta, Cs,
-                n, 0)
-    rate = 2.0 * r0 * n * k / max(time.perf_counter() - t, 1e-6)
+    fp32 = dtype == "f32"
+    tol = 1e-5 if fp32 else 1e-12
+    port_acc = 0 if fp32 else 1  # fp32: the port accumulates in fp32, as sgemm does
+
+    def run_rows(rows, acc):
+        Cs = np.array(C0[:rows * ldc], copy=True)  # the oracle writes C in place
+        t = time.perf_counter()
+        oracle.gemm(0, ta, tb, rows, n, k, alpha, A, lda, B, ldb, beta, Cs, ldc, acc)
+        return Cs, time.perf_counter() - t
+
+    r0 = min(m, 64)
+    _, dt0 = run_rows(r0, port_acc)
+    rate = 2.0 * r0 * n * k / max(dt0, 1e-6)
     rows = int(min(m, max(r0, (rate * target_s) / (2.0 * n * k) // 64 * 64)))
-    As = np.array(A[:rows * k], copy=True)
-    Cs = np.array(C0[:rows * n], copy=True)  # the oracle writes C in place
-    t = time.perf_counter()
-    oracle.gemm(0, 0, 0, rows, n, k, alpha, As, k, B, n, beta, Cs, n, 0)
-    dt = time.perf_counter() - t
+    Cp, dt = run_rows(rows, port_acc)
     value = 2.0 * rows * n * k / dt / 1e12
-    # parity on the same rows: GPU result vs oracle accumulating in double
-    Cd = np.array(C0[:rows * n], copy=True)
-    oracle.gemm(0, 0, 0, rows, n, k, alpha, As, k, B, n, beta, Cd, n, 1)
-    g = np.ascontiguousarray(got_full[:rows * n]).reshape(rows, n)
-    err_truth = oracle.rel_fro_err(g, Cd.reshape(rows, n))
-    err_port = oracle.rel_fro_err(g, Cs.reshape(rows, n))
     base = {"value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"first {rows} of {m} rows of the same {m}x{n}x{k} fp32 GEMM "
-                      f"(oracle/sbo.c blocked OpenMP sgemm, fp32 accumulation, {dt:.1f} s)",
+            "sample": f"first {rows} of {m} rows of the same {m}x{n}x{k} {dtype} GEMM "
+                      f"(tA={ta}, tB={tb}; oracle/sbo.c blocked OpenMP "
+                      f"{'sgemm, fp32' if fp32 else 'dgemm, fp64'} accumulation, {dt:.2f} s)",
             "cpu": cpu_model()}
-    # The reference's CPU GEMM is oneMKL's sgemm (unbuildable here); torch's
-    # CPU matmul is MKL sgemm, the same vendor family, so it is timed on the
-    # same rows as a closer stand-in for that path.
+    g = _host_view(got, False, m, n, ldc)
     try:
         import torch
         torch.set_num_threads(threads)
-        tA = torch.from_numpy(As.reshape(rows, k))
-        tB = torch.from_numpy(np.ascontiguousarray(B).reshape(k, n))
-        tC = torch.from_numpy(np.array(C0[:rows * n], copy=True).reshape(rows, n))
+        tA = torch.from_numpy(np.ascontiguousarray(_host_view(A, ta, m, k, lda)[:rows]))
+        tB = torch.from_numpy(np.ascontiguousarray(_host_view(B, tb, k, n, ldb)))
+        tC = torch.from_numpy(np.ascontiguousarray(_host_view(C0, False, rows, n, ldc)))
         torch.addmm(tC, tA, tB, beta=beta, alpha=alpha)  # warm-up (thread pool, packing)
         t = time.perf_counter()
         out = torch.addmm(tC, tA, tB, beta=beta, alpha=alpha)
         dt_mkl = time.perf_counter() - t
         base["mkl"] = {"value": round(2.0 * rows * n * k / dt_mkl / 1e12, 4), "unit": "TFLOP/s",
                        "cores": threads,
-                       "what": f"torch.addmm on the CPU (BLAS_INFO=mkl: MKL sgemm), "
-                               f"same rows, {dt_mkl:.2f} s",
-                       "normwise_vs_gpu": oracle.rel_fro_err(out.numpy(), g)}
+                       "what": f"torch.addmm on the CPU (BLAS_INFO=mkl: MKL "
+                               f"{'sgemm' if fp32 else 'dgemm'}), same rows, {dt_mkl:.3f} s",
+                       "normwise_vs_gpu": oracle.rel_fro_err(out.numpy(), np.ascontiguousarray(g[:rows]))}
     except Exception as e:  # the port above is the required baseline; this one is extra
         base["mkl"] = {"error": str(e)[:200]}
-    parity = {"rows": rows, "normwise_vs_oracle_f64acc": err_truth,
-              "normwise_vs_oracle_f32acc": err_port, "tolerance": 1e-5}
+    # parity over the whole matrix against the double-accumulating oracle
+    if not fp32 and rows == m:
+        Cd = Cp  # the fp64 port already accumulates in double
+    else:
+        Cd, _ = run_rows(m, 1)
+    truth = np.ascontiguousarray(_host_view(Cd, False, m, n, ldc))
+    g = np.ascontiguousarray(g)
+    err_truth = oracle.rel_fro_err(g, truth)
+    err_port = oracle.rel_fro_err(np.ascontiguousarray(g[:rows]),
+                                  np.ascontiguousarray(_host_view(Cp, False, rows, n, ldc)))
+    parity = {"rows": m, "normwise_vs_oracle_f64acc": err_truth,
+              "port_rows": rows, "normwise_vs_port": err_port, "tolerance": tol,
+              "ok": bool(err_truth <= tol)}
     return base, parity
 
 
@@ -218,8 +245,12 @@ def vendor_headline(A, B, C, m, n, k, alpha, beta, steps, warmup):
         return {"error": str(e)[:200]}
 
 
-def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup, dist="uniform"):
-    """Allocate, fill and time one GEMM configuration; returns a dict."""
+def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup, dist="uniform",
+               cpu_s=None):
+    """Allocate, fill and time one GEMM configuration; returns a dict.  With
+    cpu_s (row-major only), the result of one call on the initial C is
+    checked against the oracle over the whole matrix (`parity`) and the CPU
+    path is timed on a sample of about cpu_s seconds (`cpu_baseline`)."""
     import torch
     import sushiblas_amd as sbx
     tdt = torch.float32 if dtype == "f32" else torch.float64
@@ -248,6 +279,13 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
     def step():
         sbx.gemm_ex(sdt, layout, ta, tb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0)
 
+    host = None
+    if cpu_s is not None and layout == 0:
+        torch.cuda.synchronize()
+        host = (A.cpu().numpy(), B.cpu().numpy(), C.cpu().numpy())
+        step()
+        torch.cuda.synchronize()
+        host = host + (C.cpu().numpy(),)
     ms = time_launches(step, steps, warmup, min_warm_s=0.25)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
@@ -272,6 +310,10 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
             out["vendor_error"] = str(e)[:200]
     del A, B, C
     torch.cuda.empty_cache()
+    if host is not None:
+        out["cpu_baseline"], out["parity"] = cpu_leg(dtype, ta, tb, m, n, k, alpha, beta,
+                                                     host[0], lda, host[1], ldb, host[2], ldc,
+                                                     host[3], cpu_s)
     return out
 
 
@@ -379,24 +421,25 @@ def engine_patterns():
     return out
 
 
-def secondary_workloads(steps_arg):
-    """The `also` workloads in run order, as key -> thunk."""
+def secondary_workloads(steps_arg, cpu_s=None):
+    """The `also` workloads in run order, as key -> thunk.  cpu_s: CPU sample
+    seconds for each BASELINE GEMM config's cpu_baseline / parity (None: skip)."""
     steps = max(3, min(steps_arg, 10))
     w = {}
     w["fp64_8192_cfg5"] = lambda: run_config("f64", 0, 0, 0, 8192, 8192, 8192, 1.0, 0.0,
-                                             SEED + 5, steps, 2)
+                                             SEED + 5, steps, 2, cpu_s=cpu_s)
     for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
         w[f"fp32_ragged_cfg3_t{ta}{tb}"] = (lambda ta=ta, tb=tb: run_config(
-            "f32", 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3, steps, 2))
+            "f32", 0, ta, tb, 4095, 3001, 2047, 1.0, 1.0, SEED + 3, steps, 2, cpu_s=cpu_s))
 
     def tall_skinny():
         ts = run_config("f32", 0, 0, 0, 65536, 64, 4096, 1.0, 0.0, SEED + 4, steps, 2,
-                        dist="tall_skinny")
+                        dist="tall_skinny", cpu_s=cpu_s)
         ts["hbm_frac"] = round(ts["hbm_gbs"] / HBM_PEAK_GBS, 4)
         return ts
     w["fp32_tall_skinny_cfg4"] = tall_skinny
     w["fp32_512_cfg1"] = lambda: run_config("f32", 0, 0, 0, 512, 512, 512, 1.0, 0.0, SEED + 1,
-                                            steps * 5, 5)
+                                            steps * 5, 5, cpu_s=cpu_s)
     w["fp32_gemm_relu_layer_512x1024x1024"] = lambda: run_fused_config(
         512, 1024, 1024, SEED + 6, steps * 5, 5)
     w["fp32_gemm_relu_8192x8192x256"] = lambda: run_fused_config(8192, 8192, 256, SEED + 7,
@@ -427,7 +470,7 @@ def main():
     if args.only:
         import sushiblas_amd as sbx
         sbx.lib()
-        work = secondary_workloads(args.steps)
+        work = secondary_workloads(args.steps, None if args.no_cpu else args.cpu_seconds)
         if args.only not in work:
             print(f"unknown workload {args.only!r}; one of: {', '.join(work)}", file=sys.stderr)
             sys.exit(2)
@@ -495,8 +538,8 @@ def main():
     if need_host:
         del A, B
         torch.cuda.empty_cache()
-        base, parity = cpu_baseline(A_h, B_h, C0_h, m, n, k, alpha, beta, got_h,
-                                    args.cpu_seconds)
+        base, parity = cpu_leg("f32", 0, 0, m, n, k, alpha, beta, A_h, k, B_h, n, C0_h, n,
+                               got_h, args.cpu_seconds)
         result["cpu_baseline"] = base
         result["parity"] = parity
     else:
@@ -506,7 +549,8 @@ def main():
 
     if not args.no_also:
         also = {}
-        for key, fn in secondary_workloads(args.steps).items():
+        for key, fn in secondary_workloads(args.steps,
+                                           None if args.no_cpu else args.cpu_seconds).items():
             also[key] = fn()
             if key != "engine_task_graph":
                 also[key]["traffic"] = read_traffic(key)

@@ -345,6 +345,12 @@ struct Frag {
     static constexpr int V = Mfma<T>::V;
     static constexpr int U = KC ? 1 : (NB < V ? NB : V);  // interleave factor
     static_assert(NB % U == 0, "block count must be a multiple of the interleave");
+    // LDS read instructions per k group: a k-contiguous tile takes one
+    // 16-byte read per block; an x-contiguous one NB/U*V reads of U elements,
+    // which the compiler pairs into ds_read2 instructions when they are
+    // narrower than 16 bytes (rows kk and kk+1 lie LD elements apart)
+    static constexpr int INSTR =
+        KC ? NB : (NB / U * V) / (U * (int)sizeof(T) < 16 ? 2 : 1);
 
     // Read the fragments of k-group g (8 k values) for wave offset w0.
     // f[b][kk] is block b's operand for MFMA step kk.
@@ -547,7 +553,9 @@ gemm_mfma_kernel(GemmArgs<T> p)
 
     // Instruction counts that the scheduling hints below interleave.
     constexpr int MPG = NBM * NBN * V;  // MFMAs per k group
-    constexpr int RPG = (A_KC ? NBM : NBM / FragA::U * V) + (B_KC ? NBN : NBN / FragB::U * V);
+    // (fragment reads counted as the instructions the compiler emits: a hint
+    // pattern that asks for more reads than exist does not take hold)
+    constexpr int RPG = FragA::INSTR + FragB::INSTR;
     constexpr int NLD = OpA::NV + OpB::NV;  // global loads (= LDS writes) per tile
     static_assert(G % 2 == 0, "fragment double-buffering needs an even number of k groups");
 

@@ -88,8 +88,9 @@ const CfgInfo kCfg[] = {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Tile configurations worth modelling for a problem, the default first.
-int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
+// Tile configurations worth modelling for a problem, the default first; cus
+// is the device's CU count (the round size of one-per-CU tiles).
+int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out)
 {
     if (uplo) {
         // a triangle needs square tiles, so diagonal tiles are the tm == tn ones
@@ -99,7 +100,7 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
         }
         int c = 0;
         const int64_t t = cdiv(n, 256);
-        if (t * (t + 1) / 2 >= 256) out[c++] = F32_256x256;
+        if (t * (t + 1) / 2 >= cus) out[c++] = F32_256x256;
         // three per CU before two: timed on 8 triangles (1000..8192), the
         // pick is then within 2.6 % of the fastest (8.2 % the other way)
         out[c++] = F32_128x128_O3;
@@ -114,11 +115,11 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, Cfg* out)
     if (n <= 64) {
         // one 8-wave 256-row workgroup per CU: B is read by half as many
         // workgroups (65536 x 64 x 4096: 291-294 us against 296-300)
-        if (f32 && cdiv(m, 256) >= 256) out[c++] = F32_256x64;
+        if (f32 && cdiv(m, 256) >= cus) out[c++] = F32_256x64;
         out[c++] = tall;
     } else if (m <= 64) {
         out[c++] = wide;
-    } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= 192) {
+    } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= cus * 3 / 4) {
         out[c++] = F32_256x256;  // (nearly) full rounds of the largest tile
         // three 128^2 workgroups per CU beat it where the 256^2 grid ends
         // in a ragged round or a ragged tile (5000^2 x 1000: 394 vs 450 us)
@@ -484,8 +485,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     SplitPlan sp{0, 1, 0};
     if (algo != SBX_ALGO_GENERIC) {
         Cfg cands[5];
-        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cands);
         const int64_t cus = cu_count();
+        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands);
         bool any = false;
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
         for (int i = 0; i < nc; ++i) {

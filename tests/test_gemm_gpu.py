@@ -87,9 +87,10 @@ def test_cfg4_tall_skinny(cuda):
     del torch
 
 
-def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c):
-    """Full-size GEMM on the GPU; oracle on a sample of rows plus a
-    Freivalds projection of the whole result (C_gpu x vs alpha A (B x) + beta C0 x)."""
+def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c, all_rows=False):
+    """Full-size GEMM on the GPU; the oracle (accumulating in double) on a
+    sample of rows -- or on every row with all_rows -- plus a Freivalds
+    projection of the whole result (C_gpu x vs alpha A (B x) + beta C0 x)."""
     import torch
     import sushiblas_amd as sbx
     tdt = torch.float32 if dtype == np.float32 else torch.float64
@@ -110,8 +111,11 @@ def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c):
                 dB, n, 0, beta, dC, n, 0)
     torch.cuda.synchronize()
     got = dC.cpu().numpy().reshape(m, n)
-    rows = np.unique(np.concatenate([np.arange(0, 16), np.arange(m - 16, m),
-                                     np.random.default_rng(seed).integers(0, m, 32)]))
+    if all_rows:
+        rows = np.arange(m)
+    else:
+        rows = np.unique(np.concatenate([np.arange(0, 16), np.arange(m - 16, m),
+                                         np.random.default_rng(seed).integers(0, m, 32)]))
     Ar = np.ascontiguousarray(A.reshape(m, k)[rows]).ravel()
     Cr = np.ascontiguousarray(C0.reshape(m, n)[rows]).ravel()
     oracle.gemm(0, 0, 0, len(rows), n, k, alpha, Ar, k, B, n, beta, Cr, n, 1)
@@ -121,25 +125,45 @@ def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c):
     rhs = alpha * (A.reshape(m, k).astype(np.float64) @ (B.reshape(k, n).astype(np.float64) @ x))
     rhs += beta * (C0.reshape(m, n).astype(np.float64) @ x)
     err_proj = float(np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs))
-    print(f"{m}x{n}x{k} {np.dtype(dtype).name}: sampled-rows err={err_rows:.3e} "
+    print(f"{m}x{n}x{k} {np.dtype(dtype).name}: {len(rows)} rows err={err_rows:.3e} "
           f"Freivalds err={err_proj:.3e}", flush=True)
     return err_rows, err_proj
 
 
 def test_cfg2_fp32_8192(cuda):
-    """fp32 8192^3, alpha=1.5, beta=0.5, C ~ N(0,1): sampled rows + Freivalds."""
+    """fp32 8192^3, alpha=1.5, beta=0.5, C ~ N(0,1): the whole matrix against
+    the oracle, plus Freivalds."""
     e_rows, e_proj = _sampled_rows_check(cuda, np.float32, 8192, 8192, 8192, 1.5, 0.5,
-                                         SEED + 2, "normal")
+                                         SEED + 2, "normal", all_rows=True)
     assert e_rows <= TOL[np.float32]
     assert e_proj <= TOL[np.float32]
 
 
 def test_cfg5_fp64_8192(cuda):
-    """fp64 8192^3, alpha=1, beta=0: sampled rows + Freivalds, tolerance 1e-12."""
+    """fp64 8192^3, alpha=1, beta=0: the whole matrix against the oracle, plus
+    Freivalds, tolerance 1e-12."""
     e_rows, e_proj = _sampled_rows_check(cuda, np.float64, 8192, 8192, 8192, 1.0, 0.0,
-                                         SEED + 5, "uniform")
+                                         SEED + 5, "uniform", all_rows=True)
     assert e_rows <= TOL[np.float64]
     assert e_proj <= TOL[np.float64]
+
+
+def test_operand_above_2gib(cuda):
+    """An A of 2.25 GiB (147456 x 4096 fp32) through the MFMA tile path: the
+    buffer descriptor's record count saturates at 2^31 - 16 bytes, so tiles
+    past 2 GiB must be reached through the per-tile moving base.  Sampled
+    rows (including the last 16) against the oracle, plus Freivalds over the
+    whole result."""
+    import sushiblas_amd as sbx
+    m, n, k = 147456, 64, 4096
+    assert m * k * 4 > (2 << 30)
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+    print(f"above-2GiB case {m}x{n}x{k} -> {name}", flush=True)
+    assert name.startswith("mfma_"), name
+    e_rows, e_proj = _sampled_rows_check(cuda, np.float32, m, n, k, 1.0, 0.5, SEED + 6,
+                                         "uniform")
+    assert e_rows <= TOL[np.float32]
+    assert e_proj <= TOL[np.float32]
 
 
 # -- coverage sweeps -----------------------------------------------------------
@@ -434,6 +458,30 @@ def test_tall_skinny_eight_wave_tile(cuda, ta, tb):
         assert name.startswith("mfma_f32_256x64x32_w8x1"), name
         got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
+    """The 8-wave 256x64 tile where its grid is not one whole round:
+    80000 x 64 x 2048 runs 256 whole tiles plus a 57-tile tail cut 4 ways
+    (its split partials fill 16384-element workspace slots and the reduction
+    walks 64 chunks of each), and 100000 x 63 x 515 runs 391 tiles unsplit
+    (a partial second round, a ragged last row tile, n = 63 and a K tail).
+    Padded leading dimensions; the ldc padding of C stays untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k, want_name) in enumerate([
+            (80000, 64, 2048, "mfma_f32_256x64x32_w8x1+splitk4"),
+            (100000, 63, 515, "mfma_f32_256x64x32_w8x1")]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 96 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == want_name, name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.75, A, lda, B, ldb, 1.5, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, -0.75, A, lda, B, ldb, 1.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
         np.testing.assert_array_equal(got[outside], C[outside])
