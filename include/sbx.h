@@ -111,6 +111,29 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
                 int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
                 void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo);
 
+/* Bytes of the fixed per-device scratch that sbx_gemm_ex_noalloc uses. */
+#define SBX_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* sbx_gemm_ex without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments and results as sbx_gemm_ex, except that split-K partials go to a
+ * fixed array of SBX_NOALLOC_SCRATCH_BYTES in device memory (one per GPU,
+ * held from the library's first use on that GPU until the process ends)
+ * instead of the stream's workspace, and the tiling heuristics only consider
+ * splits whose partials fit in it (a problem whose preferred split would not
+ * fit runs with fewer k-parts or unsplit, so results may differ from
+ * sbx_gemm_ex by rounding only; none is refused for its size).  It calls no
+ * hipMalloc/hipFree.  Every call on one GPU shares that GPU's array: calls
+ * whose split kernels overlap on one GPU (different streams, not ordered by
+ * the caller) race on it; calls ordered on one stream do not.  Every partial
+ * is written before it is read, so nothing in the array needs clearing. */
+int sbx_gemm_ex_noalloc(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                        int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                        int64_t str_a, const void* B, int64_t ldb, int64_t str_b,
+                        const void* beta, void* C, int64_t ldc, int64_t str_c, int64_t batch,
+                        int algo);
+
 /* Epilogues that can be fused into the GEMM (no counterpart on the
  * reference's GEMM path, where they are separate tasks). */
 typedef enum sbx_epilogue { SBX_EPILOGUE_NONE = 0, SBX_EPILOGUE_RELU = 1 } sbx_epilogue;

@@ -73,6 +73,8 @@ def lib() -> ctypes.CDLL:
         f.restype = i32
         f.argtypes = [vp, i32, i32, i32, i64, i64, i64, real, vp, i64, i64, vp, i64, i64, real,
                       vp, i64, i64, i64]
+    L.sbx_gemm_ex_noalloc.restype = i32
+    L.sbx_gemm_ex_noalloc.argtypes = L.sbx_gemm_ex.argtypes
     L.sbx_gemm_fused.restype = i32
     L.sbx_gemm_fused.argtypes = [vp, i32, i32, i32, i32, i64, i64, i64, vp, vp, i64, i64, vp,
                                  i64, i64, vp, vp, i64, i64, i64, i32]
@@ -149,6 +151,20 @@ def gemm_ex(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb
                            k, ctypes.byref(a), _ptr(A), lda, str_a, _ptr(B), ldb, str_b,
                            ctypes.byref(b), _ptr(C), ldc, str_c, batch, algo)
     _check(st, "sbx_gemm_ex")
+
+
+def gemm_ex_noalloc(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb, str_b,
+                    beta, C, ldc, str_c, batch=1, algo=ALGO_AUTO, stream=None) -> None:
+    """sbx_gemm_ex_noalloc: sbx_gemm_ex with split-K partials in the fixed
+    per-device scratch (no allocation)."""
+    real = ctypes.c_float if dtype == F32 else ctypes.c_double
+    a = real(alpha)
+    b = real(beta)
+    st = lib().sbx_gemm_ex_noalloc(_stream(stream), dtype, int(layout), int(transA),
+                                   int(transB), m, n, k, ctypes.byref(a), _ptr(A), lda, str_a,
+                                   _ptr(B), ldb, str_b, ctypes.byref(b), _ptr(C), ldc, str_c,
+                                   batch, algo)
+    _check(st, "sbx_gemm_ex_noalloc")
 
 
 def gemm_fused(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb, str_b,

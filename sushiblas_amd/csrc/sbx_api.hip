@@ -244,7 +244,9 @@ constexpr double kSmallRate = 0.21e12;
 constexpr double kSmallCuRate = 0.31e12;
 constexpr double kSmallF64Rate = 0.7;
 
-Choice model_plan(const Problem& p, Cfg c, int64_t cus)
+// max_ws: the most split-partial bytes a plan may use (the allocation-free
+// entry point's scratch size; unlimited otherwise).
+Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws)
 {
     if (c == F32_SMALL || c == F64_SMALL) {
         // one launch, no split; the operands' layout hardly matters
@@ -273,6 +275,7 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus)
     const int64_t full = tiles - rem;
     const int64_t smax = nk / 2 < kMaxSplit ? nk / 2 : kMaxSplit;
     for (int64_t sp = 2; sp <= smax; ++sp) {
+        if ((size_t)(rem * sp) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
         const double t = rounds_time(full, w, P, cus, e1) +
                          rounds_time(rem * sp, w / (double)sp, P, cus, e1) + F + G +
                          (double)(rem * sp) * ci.bm * ci.bn * elem / W;
@@ -475,9 +478,11 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Pr
     }
 }
 
+// fixed_ws / fixed_bytes: caller-provided split workspace (the
+// allocation-free entry point's scratch); null: the stream's cached one.
 template <typename T>
 int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen,
-        SplitPlan* chosen_split)
+        SplitPlan* chosen_split, void* fixed_ws = nullptr, size_t fixed_bytes = 0)
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
@@ -494,7 +499,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL;
             if (algo == SBX_ALGO_MFMA_TILE && small) continue;
             if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
-            const Choice c = model_plan(p, cands[i], cus);
+            const Choice c = model_plan(p, cands[i], cus, fixed_ws ? fixed_bytes : SIZE_MAX);
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;
         }
@@ -519,8 +524,14 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
     void* ws = nullptr;
     WorkspaceLease lease;  // held until both split kernels are enqueued
-    if (sp.split > 1) {
-        if (lease.acquire(stream, (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T)))
+    const size_t ws_bytes = (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T);
+    if (sp.split > 1 && fixed_ws) {
+        // the planner keeps every split's partials within fixed_bytes; a plan
+        // that did not fit would be refused here, never written past the end
+        if (ws_bytes > fixed_bytes) return SBX_UNSUPPORTED;
+        ws = fixed_ws;
+    } else if (sp.split > 1) {
+        if (lease.acquire(stream, ws_bytes))
             ws = lease.ptr;
         else
             sp = SplitPlan{(int)tiles, 1, 0};  // no memory: run unsplit
@@ -567,7 +578,8 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
               int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
               int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
               void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, int epilogue,
-              Cfg* chosen, SplitPlan* chosen_split)
+              Cfg* chosen, SplitPlan* chosen_split, void* fixed_ws = nullptr,
+              size_t fixed_bytes = 0)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
@@ -615,9 +627,9 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen,
-                          chosen_split);
+                          chosen_split, fixed_ws, fixed_bytes);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
-                       chosen_split);
+                       chosen_split, fixed_ws, fixed_bytes);
 }
 
 // Grouped GEMM: `count` problems of one shape and one set of scalars whose
@@ -788,6 +800,36 @@ int gemv_impl(void* stream, int dtype, int layout, int trans, int64_t m, int64_t
                             (const double*)x, incx, *(const double*)beta, (double*)y, incy);
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (sbx_gemm_ex_noalloc): split-K
+// partials go to this fixed array instead of the stream workspace, so that
+// entry point makes no allocation.  Each device holds its own copy from the
+// library's first use on it until the process ends.  In host code `scratch`
+// names a host-side stand-in, not a device address: the device address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that address is ever passed to kernels.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = SBX_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes % 256 == 0, "scratch size must keep partial slots aligned");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[64] = {nullptr};
+
+// The current device's address of `scratch`; null if the lookup fails.
+void* device_scratch()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> g(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace
 }  // namespace sbx
 
@@ -802,6 +844,20 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
     return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
                           B, ldb, str_b, beta, C, ldc, str_c, batch, algo, SBX_EPILOGUE_NONE,
                           nullptr, nullptr);
+}
+
+int sbx_gemm_ex_noalloc(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                        int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                        int64_t str_a, const void* B, int64_t ldb, int64_t str_b,
+                        const void* beta, void* C, int64_t ldc, int64_t str_c, int64_t batch,
+                        int algo)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    void* ws = sbx::device_scratch();
+    if (!ws) return SBX_HIP_ERROR;
+    return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, algo, SBX_EPILOGUE_NONE,
+                          nullptr, nullptr, ws, sbx::kScratchBytes);
 }
 
 int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, int64_t m,

@@ -1,0 +1,111 @@
+"""GPU tests of the allocation-free entry point sbx_gemm_ex_noalloc
+(include/sbx.h): split-K partials in the fixed per-device scratch array
+instead of the stream workspace.  It has no counterpart in the reference; it
+must give sbx_gemm_ex's results (bit for bit where both plan the same split,
+within the fp32/fp64 tolerance where the scratch bounds the split) and must
+not allocate device memory.
+
+Bar: normwise relative Frobenius error against the oracle accumulating in
+double <= 1e-5 (fp32) / 1e-12 (fp64), as for every GEMM test.
+"""
+import numpy as np
+import pytest
+
+from gemm_cases import TOL, make_inputs, normwise, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261277
+SCRATCH = 32 << 20  # SBX_NOALLOC_SCRATCH_BYTES
+
+
+def _run_both(cuda, dtype, m, n, k, alpha, beta, seed, stream):
+    """The same problem through sbx_gemm_ex and sbx_gemm_ex_noalloc (same
+    input bits, separate outputs) plus the oracle; host results."""
+    import torch
+    import sushiblas_amd as sbx
+    A, lda, B, ldb, C, ldc = make_inputs(dtype, 0, 0, 0, m, n, k, seed)
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    dA = torch.from_numpy(A).to(cuda)
+    dB = torch.from_numpy(B).to(cuda)
+    c_ref = torch.from_numpy(C).to(cuda)
+    c_na = torch.from_numpy(C).to(cuda)
+    torch.cuda.synchronize()
+    sbx.gemm_ex(code, 0, 0, 0, m, n, k, alpha, dA, lda, 0, dB, ldb, 0, beta, c_ref, ldc, 0,
+                stream=stream)
+    sbx.gemm_ex_noalloc(code, 0, 0, 0, m, n, k, alpha, dA, lda, 0, dB, ldb, 0, beta, c_na, ldc,
+                        0, stream=stream)
+    torch.cuda.synchronize()
+    want = run_oracle(0, 0, 0, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+    return c_ref.cpu().numpy(), c_na.cpu().numpy(), want, ldc
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_noalloc_matches_gemm_ex_two_calls(cuda, dtype):
+    """Two calls in a row on one stream, the second on a smaller problem:
+    both split K, both fit the scratch, so the plans and the bits match
+    sbx_gemm_ex's; both are within tolerance of the oracle."""
+    import torch
+    import sushiblas_amd as sbx
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    stream = torch.cuda.Stream()
+    shapes = ([(1536, 1536, 1024), (384, 320, 3000)] if dtype == np.float32
+              else [(512, 384, 2048), (384, 320, 3000)])
+    for i, (m, n, k) in enumerate(shapes):
+        name = sbx.gemm_select(code, 0, 0, 0, m, n, k, k, n, n)
+        print(f"noalloc case {np.dtype(dtype).name} {m}x{n}x{k} -> {name}", flush=True)
+        assert "+splitk" in name, name
+        ref, got, want, ldc = _run_both(cuda, dtype, m, n, k, 1.25, -0.5, SEED + i, stream)
+        np.testing.assert_array_equal(got.view(np.uint8), ref.view(np.uint8))
+        assert normwise(0, got, want, m, n, ldc) <= TOL[dtype]
+
+
+def test_noalloc_bounds_the_split_to_the_scratch(cuda):
+    """A problem whose preferred split needs more than the scratch (32 tail
+    tiles of 256x256 cut 5+ ways: > 32 MiB of partials) runs with a split
+    that fits; the result stays within tolerance of the oracle and of
+    sbx_gemm_ex.  A second, smaller call follows."""
+    import torch
+    import sushiblas_amd as sbx
+    stream = torch.cuda.Stream()
+    m, n, k = 4608, 4096, 512
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+    parts = int(name.split("splitk")[1])
+    assert name.startswith("mfma_f32_256x256") and 32 * parts * 256 * 256 * 4 > SCRATCH, name
+    for i, (mm, nn, kk) in enumerate([(m, n, k), (512, 512, 2048)]):
+        ref, got, want, ldc = _run_both(cuda, np.float32, mm, nn, kk, 1.0, 0.5, SEED + 10 + i,
+                                        stream)
+        err = normwise(0, got, want, mm, nn, ldc)
+        print(f"noalloc bounded case {mm}x{nn}x{kk} err={err:.3e}", flush=True)
+        assert err <= TOL[np.float32]
+        assert normwise(0, got, ref, mm, nn, ldc) <= TOL[np.float32]
+
+
+def test_noalloc_allocates_nothing(cuda):
+    """On a stream it has never seen, a split-K call of sbx_gemm_ex_noalloc
+    takes no device memory (sbx_gemm_ex would allocate that stream's
+    workspace, at least 32 MiB, unless a pooled one is free)."""
+    import torch
+    import sushiblas_amd as sbx
+    m, n, k = 1536, 1536, 1024
+    assert "+splitk" in sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+    A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 20)
+    dA = torch.from_numpy(A).to(cuda)
+    dB = torch.from_numpy(B).to(cuda)
+    dC = torch.from_numpy(C).to(cuda)
+    # First use on this device resolves the scratch address; the first
+    # launches on a new stream let the HIP runtime set that stream up (its own
+    # lazy allocations, a few MiB).  Neither is measured: a 64^3 problem runs
+    # unsplit, so it touches no scratch either way.
+    fresh = torch.cuda.Stream()
+    for _ in range(2):
+        sbx.gemm_ex_noalloc(sbx.F32, 0, 0, 0, 64, 64, 64, 1.0, dA, lda, 0, dB, ldb, 0, 0.0, dC,
+                            ldc, 0, stream=fresh)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        sbx.gemm_ex_noalloc(sbx.F32, 0, 0, 0, m, n, k, 1.0, dA, lda, 0, dB, ldb, 0, 0.0, dC,
+                            ldc, 0, stream=fresh)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free0 - free1 < (1 << 20), (free0, free1)
