@@ -320,14 +320,17 @@ struct Operand {
     // check is per dword): zero them.  An x-contiguous vector that straddles
     // the X extent needs nothing -- those elements only reach C rows/columns
     // that are never stored -- and its k index is one row, checked at load.
-    template <int S>
+    // MASK: apply the k-tail zeroing (only the last k tile of K can hold a
+    // straddling vector, so the k loop stores unmasked and only its peeled
+    // tail masks)
+    template <int S, bool MASK = true>
     __device__ inline void store(T* lds)
     {
         constexpr int DPE = (int)sizeof(T) / 4;  // dwords per element
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             raw_t w = stage[S][j];
-            if constexpr (KC && KTAIL) {
+            if constexpr (KC && KTAIL && MASK) {
                 const int lim = krem[S] - kidx(j);  // elements of vector j inside K
 #pragma unroll
                 for (int d = DPE; d < VEC * DPE; ++d)
@@ -530,9 +533,10 @@ gemm_mfma_kernel(GemmArgs<T> p)
             make_rsrc(B + pb, b_span - pb * (int64_t)sizeof(T)), k_rem);
     };
     // staging set S -> LDS buffer buf
-    auto commit = [&](auto S, int buf) {
-        opa.template store<decltype(S)::value>(smem + buf * OpA::ELEMS);
-        opb.template store<decltype(S)::value>(smem + 2 * OpA::ELEMS + buf * OpB::ELEMS);
+    auto commit = [&](auto S, int buf, auto MASK) {
+        constexpr bool mask = decltype(MASK)::value;
+        opa.template store<decltype(S)::value, mask>(smem + buf * OpA::ELEMS);
+        opb.template store<decltype(S)::value, mask>(smem + 2 * OpA::ELEMS + buf * OpB::ELEMS);
     };
 
     T fa[2][NBM][V], fb[2][NBN][V];  // fragments, double-buffered across k groups
@@ -573,7 +577,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // that each region is one basic block the scheduling hints can interleave:
     // past the last k tile the buffer loads are masked (k_rem <= 0 or the
     // next part's data) and what they write to the idle LDS buffer is unused.
-    auto step = [&](auto S, int kt, int cur) {
+    auto step = [&](auto S, int kt, int cur, auto MASK) {
         constexpr int st = decltype(S)::value;
         issue(Int<st>{}, kt + PF);
 #pragma unroll
@@ -583,7 +587,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
             if ((g & 1) == 0) mma(Int<0>{});
             else mma(Int<1>{});
         }
-        commit(Int<(st + 1) % PF>{}, cur ^ 1);
+        commit(Int<(st + 1) % PF>{}, cur ^ 1, MASK);
         // region A: loads first, then fragment reads, then the LDS writes,
         // each memory instruction followed by a slice of the MFMAs
         {
@@ -625,26 +629,54 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // prologue: tile kt0 -> set 0 -> LDS buffer 0; tiles kt0+1 .. kt0+PF-1
     // -> sets 1 .. PF-1
     issue(Int<0>{}, kt0);
-    commit(Int<0>{}, 0);
+    commit(Int<0>{}, 0, std::true_type{});
     if constexpr (PF > 1) issue(Int<1>{}, kt0 + 1);
     if constexpr (PF > 2) issue(Int<2>{}, kt0 + 2);
     if constexpr (PF > 3) issue(Int<3>{}, kt0 + 3);
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
 
-    if constexpr (PF == 1) {
-        for (int kt = kt0; kt < nk; ++kt) step(Int<0>{}, kt, (kt - kt0) & 1);
+    if constexpr (!KTAIL) {
+        if constexpr (PF == 1) {
+            for (int kt = kt0; kt < nk; ++kt) step(Int<0>{}, kt, (kt - kt0) & 1, std::false_type{});
+        } else {
+            for (int kt = kt0; kt < nk; kt += PF) {
+                const int cur = (kt - kt0) & 1;
+                step(Int<0>{}, kt, cur, std::false_type{});
+                if (kt + 1 < nk) step(Int<1 % PF>{}, kt + 1, cur ^ 1, std::false_type{});
+                if constexpr (PF > 2) {
+                    if (kt + 2 < nk) step(Int<2 % PF>{}, kt + 2, cur, std::false_type{});
+                }
+                if constexpr (PF > 3) {
+                    if (kt + 3 < nk) step(Int<3 % PF>{}, kt + 3, cur ^ 1, std::false_type{});
+                }
+            }
+        }
     } else {
-        for (int kt = kt0; kt < nk; kt += PF) {
+        // Step kt stores tile kt + 1 to LDS, and only tile nk - 1 can hold
+        // a vector that straddles K, so the loop runs its steps unmasked up
+        // to step nk - 3 and the remaining steps (fewer than PF + 2) run
+        // once, masked, after it: no branch inside the loop.
+        int kt = kt0;
+        for (; kt + PF <= nk - 2; kt += PF) {
             const int cur = (kt - kt0) & 1;
-            step(Int<0>{}, kt, cur);
-            if (kt + 1 < nk) step(Int<1 % PF>{}, kt + 1, cur ^ 1);
-            if constexpr (PF > 2) {
-                if (kt + 2 < nk) step(Int<2 % PF>{}, kt + 2, cur);
-            }
-            if constexpr (PF > 3) {
-                if (kt + 3 < nk) step(Int<3 % PF>{}, kt + 3, cur ^ 1);
-            }
+            step(Int<0>{}, kt, cur, std::false_type{});
+            if constexpr (PF > 1) step(Int<1 % PF>{}, kt + 1, cur ^ 1, std::false_type{});
+            if constexpr (PF > 2) step(Int<2 % PF>{}, kt + 2, cur, std::false_type{});
+            if constexpr (PF > 3) step(Int<3 % PF>{}, kt + 3, cur ^ 1, std::false_type{});
+        }
+        // the rest, staging sets 0, 1, ... in order
+        const int cur = (kt - kt0) & 1;
+        if (kt < nk) step(Int<0>{}, kt, cur, std::true_type{});
+        if (kt + 1 < nk) step(Int<1 % PF>{}, kt + 1, cur ^ 1, std::true_type{});
+        if constexpr (PF > 1) {
+            if (kt + 2 < nk) step(Int<2 % PF>{}, kt + 2, cur, std::true_type{});
+        }
+        if constexpr (PF > 2) {
+            if (kt + 3 < nk) step(Int<3 % PF>{}, kt + 3, cur ^ 1, std::true_type{});
+        }
+        if constexpr (PF > 3) {
+            if (kt + 4 < nk) step(Int<4 % PF>{}, kt + 4, cur, std::true_type{});
         }
     }
 
