@@ -16,8 +16,9 @@
 //      "k-contiguous"  tile (A not transposed / B transposed): [X][BK + PAD]
 //      "x-contiguous"  tile (A transposed / B not transposed): [BK][X]
 //  * Fragments are read with one 16-byte LDS read per lane.  The MFMA k index
-//    is a permutation of the real k inside each group of 8: lane group q at
-//    MFMA step kk uses k = 8g + V*q + kk (V = 16 bytes / sizeof(T)).  For an
+//    is a permutation of the real k inside each k group of KG = Q*V values
+//    (8; 16 for the 16x16x4 fp32 shape): lane group q at MFMA step kk uses
+//    k = KG*g + V*q + kk (V = 16 bytes / sizeof(T)).  For an
 //    x-contiguous tile, U neighbouring MFMA blocks are interleaved (block u
 //    owns rows U*i + u) so that one 16-byte read feeds U blocks.
 //  * Masking: loads go through buffer resources whose base moves with the
@@ -55,17 +56,20 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
-// MFMA shapes.  fp32: v_mfma_f32_32x32x2_f32, fp64: v_mfma_f64_16x16x4_f64.
+// MFMA shapes.  fp32: v_mfma_f32_32x32x2_f32 (MI = 0) or
+// v_mfma_f32_16x16x4_f32 (MI = 1); fp64: v_mfma_f64_16x16x4_f64.
 //   A operand: lane l holds A[i = l % MB][k = l / MB]
 //   B operand: lane l holds B[k = l / MB][j = l % MB]
 //   D: lane l, accumulator r holds D[row(r, l / MB)][l % MB]
-//   (all three layouts were confirmed on the device with one-hot probes)
+//   (all layouts were confirmed on the device with one-hot probes)
+// A k group is Q * V consecutive k values: one V-wide fragment read per
+// lane feeds V MFMA steps.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int MI = 0>
 struct Mfma;
 
 template <>
-struct Mfma<float> {
+struct Mfma<float, 0> {
     static constexpr int MB = 32;    // output block edge
     static constexpr int Q = 2;      // lane groups along k (= MFMA k)
     static constexpr int V = 4;      // elements per 16-byte read
@@ -79,7 +83,21 @@ struct Mfma<float> {
 };
 
 template <>
-struct Mfma<double> {
+struct Mfma<float, 1> {
+    static constexpr int MB = 16;
+    static constexpr int Q = 4;
+    static constexpr int V = 4;
+    static constexpr int NACC = 4;
+    typedef f32x4 acc_t;
+    __device__ static inline acc_t mma(float a, float b, acc_t c)
+    {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static inline int row(int r, int q) { return 4 * q + r; }
+};
+
+template <>
+struct Mfma<double, 0> {
     static constexpr int MB = 16;
     static constexpr int Q = 4;
     static constexpr int V = 2;
@@ -342,10 +360,11 @@ struct Operand {
 };
 
 // Fragment reader for one operand of one wave: NB blocks of MB along X.
-template <typename T, int NB, bool KC, int LD>
+template <typename T, int NB, bool KC, int LD, int MI = 0>
 struct Frag {
-    static constexpr int MB = Mfma<T>::MB;
-    static constexpr int V = Mfma<T>::V;
+    static constexpr int MB = Mfma<T, MI>::MB;
+    static constexpr int V = Mfma<T, MI>::V;
+    static constexpr int KG = Mfma<T, MI>::Q * V;  // k values per group
     static constexpr int U = KC ? 1 : (NB < V ? NB : V);  // interleave factor
     static_assert(NB % U == 0, "block count must be a multiple of the interleave");
     // LDS read instructions per k group: a k-contiguous tile takes one
@@ -355,7 +374,7 @@ struct Frag {
     static constexpr int INSTR =
         KC ? NB : (NB / U * V) / (U * (int)sizeof(T) < 16 ? 2 : 1);
 
-    // Read the fragments of k-group g (8 k values) for wave offset w0.
+    // Read the fragments of k-group g (KG k values) for wave offset w0.
     // f[b][kk] is block b's operand for MFMA step kk.
     __device__ static inline void read(const T* lds, int w0, int g, int lane, T (&f)[NB][V])
     {
@@ -363,14 +382,14 @@ struct Frag {
         if (KC) {
 #pragma unroll
             for (int b = 0; b < NB; ++b)
-                LdsVec<T, V>::read(lds + (w0 + b * MB + i) * LD + g * 8 + q * V, f[b]);
+                LdsVec<T, V>::read(lds + (w0 + b * MB + i) * LD + g * KG + q * V, f[b]);
         } else {
 #pragma unroll
             for (int s = 0; s < NB / U; ++s)
 #pragma unroll
                 for (int kk = 0; kk < V; ++kk) {
                     T t[U];
-                    LdsVec<T, U>::read(lds + (g * 8 + q * V + kk) * LD + w0 + s * U * MB + U * i, t);
+                    LdsVec<T, U>::read(lds + (g * KG + q * V + kk) * LD + w0 + s * U * MB + U * i, t);
 #pragma unroll
                     for (int u = 0; u < U; ++u) f[s * U + u][kk] = t[u];
                 }
@@ -444,25 +463,27 @@ using Int = std::integral_constant<int, N>;
 // PF: global tiles in flight (1 = the next tile is fetched while the current
 // one is multiplied; 2 = the one after that too, for HBM-bound shapes).
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
+// MI: MFMA shape (see Mfma; fp32 only has a choice).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          bool KTAIL, int PF, int WPE>
+          bool KTAIL, int PF, int WPE, int MI = 0>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
-    typedef Mfma<T> MF;
+    typedef Mfma<T, MI> MF;
     constexpr int MB = MF::MB;
     constexpr int V = MF::V;
+    constexpr int KG = MF::Q * V;  // k values per group
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int NBM = WTM / MB, NBN = WTN / MB;
-    constexpr int G = BK / 8;  // k groups per tile
+    constexpr int G = BK / KG;  // k groups per tile
     constexpr int NTHR = WAVES_M * WAVES_N * 64;
     static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");
-    static_assert(BK % 8 == 0, "BK must be a multiple of the 8-wide k group");
+    static_assert(BK % KG == 0, "BK must be a multiple of the k group");
     static_assert(PF >= 1 && PF <= 4, "prefetch depth 1 to 4");
     typedef Operand<T, BM, BK, A_KC, PF, KTAIL, NTHR> OpA;
     typedef Operand<T, BN, BK, B_KC, PF, KTAIL, NTHR> OpB;
-    typedef Frag<T, NBM, A_KC, OpA::LD> FragA;
-    typedef Frag<T, NBN, B_KC, OpB::LD> FragB;
+    typedef Frag<T, NBM, A_KC, OpA::LD, MI> FragA;
+    typedef Frag<T, NBN, B_KC, OpB::LD, MI> FragB;
 
     __shared__ __attribute__((aligned(16))) T smem[2 * (OpA::ELEMS + OpB::ELEMS)];
 

@@ -1,6 +1,6 @@
 // launch.hpp -- host-side launchers for the GEMM kernels.
 //
-// launch_mfma<T, BM, BN, BK, WAVES_M, WAVES_N, PF, WPE> picks one of the 7
+// launch_mfma<T, BM, BN, BK, WAVES_M, WAVES_N, PF, WPE, MI> picks one of the 7
 // compiled variants (A k-contiguous or not, B k-contiguous or not, and for a
 // k-contiguous operand whether K needs tail masking) and launches it on
 // `stream`.
@@ -12,7 +12,7 @@
 
 namespace sbx {
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, int MI = 0>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream);
 
 // One-launch GEMM for small problems (gemm_small.hip): 32x32 tiles of C,
@@ -41,20 +41,21 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 
 // Tile configurations compiled into the library, one translation unit each
 // (gemm_cfg_*.hip instantiates launch_mfma from launch_mfma_impl.hpp):
-// (T, BM, BN, BK, waves along M, waves along N, prefetch depth, waves/SIMD)
+// (T, BM, BN, BK, waves along M, waves along N, prefetch depth, waves/SIMD,
+// MFMA shape: 0 = 32x32x2 for fp32 / 16x16x4 for fp64, 1 = 16x16x4 fp32)
 #define SBX_MFMA_CONFIGS(X)  \
-    X(float, 256, 256, 32, 4, 2, 1, 2) \
-    X(float, 128, 128, 16, 2, 2, 2, 2) \
-    X(float, 128, 128, 16, 2, 2, 2, 3) \
-    X(float, 128, 64, 32, 2, 2, 2, 2) \
-    X(float, 256, 64, 32, 8, 1, 2, 2) \
-    X(float, 64, 128, 32, 2, 2, 2, 2) \
-    X(double, 128, 128, 16, 2, 2, 1, 2) \
-    X(double, 128, 64, 16, 2, 2, 2, 2) \
-    X(double, 64, 128, 16, 2, 2, 2, 2)
+    X(float, 256, 256, 32, 4, 2, 1, 2, 0) \
+    X(float, 128, 128, 16, 2, 2, 2, 2, 0) \
+    X(float, 128, 128, 16, 2, 2, 2, 3, 0) \
+    X(float, 128, 64, 32, 2, 2, 2, 2, 0) \
+    X(float, 256, 64, 32, 8, 1, 2, 2, 1) \
+    X(float, 64, 128, 32, 2, 2, 2, 2, 0) \
+    X(double, 128, 128, 16, 2, 2, 1, 2, 0) \
+    X(double, 128, 64, 16, 2, 2, 2, 2, 0) \
+    X(double, 64, 128, 16, 2, 2, 2, 2, 0)
 
-#define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN, PF, WPE)                                        \
-    extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN, PF, WPE>(                         \
+#define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN, PF, WPE, MI)                                    \
+    extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN, PF, WPE, MI>(                     \
         const GemmArgs<T>&, bool, bool, int, hipStream_t);
 SBX_MFMA_CONFIGS(SBX_EXTERN_LAUNCH)
 #undef SBX_EXTERN_LAUNCH

@@ -7,7 +7,7 @@
 
 namespace sbx {
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, int MI>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream)
 {
     const int tiles = a.tiles;
@@ -17,7 +17,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
     // K that is not a multiple of the 16-byte vector (it costs 1-4 %)
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
 #define SBX_LAUNCH(AK, BKC, TAIL) \
-    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE><<<grid, block, 0, stream>>>(a)
+    gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE, MI><<<grid, block, 0, stream>>>(a)
     if (a_kc && b_kc) {
         if (tail) SBX_LAUNCH(true, true, true);
         else SBX_LAUNCH(true, true, false);

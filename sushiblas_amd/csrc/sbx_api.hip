@@ -58,7 +58,7 @@ enum Cfg {
     F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
     F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
-    F32_256x64,    // n <= 64 with a full round of 256-row tiles: 8 waves of 32x64
+    F32_256x64,    // n <= 64 with a full round of 256-row tiles: 8 waves of 32x64 (16x16x4 MFMAs)
     F32_64x128,    // m <= 64
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
@@ -445,7 +445,7 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
     case F32_128x64:
         return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_256x64:
-        return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2>(a, akc, bkc, nb, s);
+        return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2, 1>(a, akc, bkc, nb, s);
     case F32_64x128:
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_SMALL:
