@@ -500,6 +500,14 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             if (algo == SBX_ALGO_MFMA_TILE && small) continue;
             if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
             const Choice c = model_plan(p, cands[i], cus, fixed_ws ? fixed_bytes : SIZE_MAX);
+            // The 8-wave 256x64 tile off whole rounds only with a split
+            // tail: unsplit, its last partial round ran behind 128x64 at
+            // two per CU (100000x63x515: 86 against 82 us), which the
+            // model rates alike; with a split tail it won (80000x64x2048
+            // +splitk4: 195 against 210 us unsplit 128x64).
+            if (cands[i] == F32_256x64 && c.sp.split == 1 &&
+                tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1) % cus != 0)
+                continue;
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;
         }

@@ -468,13 +468,15 @@ def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
     """The 8-wave 256x64 tile where its grid is not one whole round:
     80000 x 64 x 2048 runs 256 whole tiles plus a 57-tile tail cut 4 ways
     (its split partials fill 16384-element workspace slots and the reduction
-    walks 64 chunks of each), and 100000 x 63 x 515 runs 391 tiles unsplit
-    (a partial second round, a ragged last row tile, n = 63 and a K tail).
+    walks 64 chunks of each), and 131000 x 63 x 515 runs two whole rounds
+    of 256 tiles (a ragged last row tile, n = 63 and a K tail).  Unsplit
+    with a partial last round, 100000 x 63 x 515 goes to the 128x64 tile.
     Padded leading dimensions; the ldc padding of C stays untouched."""
     import sushiblas_amd as sbx
     for i, (m, n, k, want_name) in enumerate([
             (80000, 64, 2048, "mfma_f32_256x64x32_w8x1+splitk4"),
-            (100000, 63, 515, "mfma_f32_256x64x32_w8x1")]):
+            (131000, 63, 515, "mfma_f32_256x64x32_w8x1"),
+            (100000, 63, 515, "mfma_f32_128x64x32_w2x2")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 96 + i,
                                              pad=(3, 1, 5))
         name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
