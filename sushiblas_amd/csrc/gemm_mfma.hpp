@@ -460,6 +460,41 @@ struct CVec<double, 2> {
 template <int N>
 using Int = std::integral_constant<int, N>;
 
+// Slice x of n items cut into `slots` near-equal slices, in order.
+__host__ __device__ constexpr int slice(int x, int n, int slots)
+{
+    return (x + 1) * n / slots - x * n / slots;
+}
+
+// Scheduling hints for one k step (see gemm_mfma_kernel's step).  Region A:
+// NLD global loads, NRD fragment reads and NLD LDS writes, in that order,
+// each followed by its slice of the region's MF MFMAs.  Region B: NRD
+// fragment reads, each followed by its slice of MF MFMAs.  The slices add up
+// to exactly the region's MFMAs: s_barrier does not bound MFMAs for the
+// scheduler, so a group that asks for more takes them from the next region
+// and pushes that region's reads to its end.
+template <int I, int NLD, int NRD, int MEM, int MF>
+__device__ inline void hints_a()
+{
+    if constexpr (I < MEM) {
+        constexpr int kind = I < NLD ? 0x020 : (I < NLD + NRD ? 0x100 : 0x200);
+        __builtin_amdgcn_sched_group_barrier(kind, 1, 0);  // VMEM read / DS read / DS write
+        constexpr int n = slice(I, MF, MEM);
+        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x008, n, 0);  // MFMA
+        hints_a<I + 1, NLD, NRD, MEM, MF>();
+    }
+}
+template <int I, int NRD, int MF>
+__device__ inline void hints_b()
+{
+    if constexpr (I < NRD) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        constexpr int n = slice(I, MF, NRD);
+        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x008, n, 0);
+        hints_b<I + 1, NRD, MF>();
+    }
+}
+
 // PF: global tiles in flight (1 = the next tile is fetched while the current
 // one is multiplied; 2 = the one after that too, for HBM-bound shapes).
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
@@ -611,40 +646,12 @@ gemm_mfma_kernel(GemmArgs<T> p)
         commit(Int<(st + 1) % PF>{}, cur ^ 1, MASK);
         // region A: loads first, then fragment reads, then the LDS writes,
         // each memory instruction followed by a slice of the MFMAs
-        {
-            constexpr int mf = (G - 1) * MPG;
-            constexpr int mem = NLD + (G - 1) * RPG + NLD;
-            constexpr int per = mf / mem > 0 ? mf / mem : 1;
-#pragma unroll
-            for (int x = 0; x < NLD; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);  // MFMA
-            }
-#pragma unroll
-            for (int x = 0; x < (G - 1) * RPG; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
-            }
-#pragma unroll
-            for (int x = 0; x < NLD; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, mf, 0);
-        }
+        hints_a<0, NLD, (G - 1) * RPG, NLD + (G - 1) * RPG + NLD, (G - 1) * MPG>();
         __syncthreads();
         read_frags(Int<0>{}, cur ^ 1, 0);
         mma(Int<1>{});
         // region B: the next tile's group-0 reads spread over the last group
-        {
-            constexpr int per = MPG / RPG > 0 ? MPG / RPG : 1;
-#pragma unroll
-            for (int x = 0; x < RPG; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, MPG, 0);
-        }
+        hints_b<0, RPG, MPG>();
     };
 
     // prologue: tile kt0 -> set 0 -> LDS buffer 0; tiles kt0+1 .. kt0+PF-1
