@@ -403,15 +403,24 @@ struct Frag {
     }
 };
 
+// Global-address-space pointer to T: epilogue loads and stores through it
+// compile to global_* instructions (flat ones also count on lgkmcnt).
+template <typename T>
+struct Glob {
+    typedef __attribute__((address_space(1))) T type;
+};
+
 // Typed vector store/load of U consecutive C elements (16 bytes for fp32 U=4).
 template <typename T, int U>
 struct CVec {
-    __device__ static inline void load(const T* p, T* o)
+    template <typename P>
+    __device__ static inline void load(const P* p, T* o)
     {
 #pragma unroll
         for (int u = 0; u < U; ++u) o[u] = p[u];
     }
-    __device__ static inline void store(T* p, const T* v)
+    template <typename P>
+    __device__ static inline void store(P* p, const T* v)
     {
 #pragma unroll
         for (int u = 0; u < U; ++u) p[u] = v[u];
@@ -419,41 +428,44 @@ struct CVec {
 };
 template <>
 struct CVec<float, 4> {
-    __device__ static inline void load(const float* p, float* o)
+    typedef Glob<f32x4>::type gv;
+    __device__ static inline void load(const Glob<float>::type* p, float* o)
     {
-        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        f32x4 v = *reinterpret_cast<const gv*>(p);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
-    __device__ static inline void store(float* p, const float* v)
+    __device__ static inline void store(Glob<float>::type* p, const float* v)
     {
         f32x4 w = {v[0], v[1], v[2], v[3]};
-        *reinterpret_cast<f32x4*>(p) = w;
+        *reinterpret_cast<gv*>(p) = w;
     }
 };
 template <>
 struct CVec<float, 2> {
-    __device__ static inline void load(const float* p, float* o)
+    typedef Glob<f32x2>::type gv;
+    __device__ static inline void load(const Glob<float>::type* p, float* o)
     {
-        f32x2 v = *reinterpret_cast<const f32x2*>(p);
+        f32x2 v = *reinterpret_cast<const gv*>(p);
         o[0] = v.x; o[1] = v.y;
     }
-    __device__ static inline void store(float* p, const float* v)
+    __device__ static inline void store(Glob<float>::type* p, const float* v)
     {
         f32x2 w = {v[0], v[1]};
-        *reinterpret_cast<f32x2*>(p) = w;
+        *reinterpret_cast<gv*>(p) = w;
     }
 };
 template <>
 struct CVec<double, 2> {
-    __device__ static inline void load(const double* p, double* o)
+    typedef Glob<f64x2>::type gv;
+    __device__ static inline void load(const Glob<double>::type* p, double* o)
     {
-        f64x2 v = *reinterpret_cast<const f64x2*>(p);
+        f64x2 v = *reinterpret_cast<const gv*>(p);
         o[0] = v.x; o[1] = v.y;
     }
-    __device__ static inline void store(double* p, const double* v)
+    __device__ static inline void store(Glob<double>::type* p, const double* v)
     {
         f64x2 w = {v[0], v[1]};
-        *reinterpret_cast<f64x2*>(p) = w;
+        *reinterpret_cast<gv*>(p) = w;
     }
 };
 
@@ -728,7 +740,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // writes them with one vector store when the destination allows it.
     constexpr int UB = FragB::U;
     const int q = lane / MB, jl = lane % MB;
-    T* dst;
+    typedef typename Glob<T>::type GT;
+    GT* dst;
     int64_t ldd;
     int row_lim, col_lim;
     T alpha, beta;
@@ -738,7 +751,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // stay (local column c of local row m is global column n0 + c, row m0 + m)
     int lo_off = -(1 << 30), hi_off = 1 << 30;
     if (is_split) {
-        dst = p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN);
+        dst = (GT*)(p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN));
         ldd = BN;
         row_lim = BM;
         col_lim = BN;
@@ -746,7 +759,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
         beta = (T)0;
         vec_ok = true;
     } else {
-        dst = C + (int64_t)m0 * p.ldc + n0;
+        dst = (GT*)(C + (int64_t)m0 * p.ldc + n0);
         ldd = p.ldc;
         row_lim = p.M - m0;
         col_lim = p.N - n0;
@@ -818,7 +831,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
                 const int c_lo = max(0, m + lo_off);
                 const int c_hi = min(col_lim, m + hi_off + 1);
                 const bool vec = UB > 1 && vec_ok && nb >= c_lo && nb + UB <= c_hi;
-                T* cp = dst + (int64_t)m * ldd + nb;
+                GT* cp = dst + (int64_t)m * ldd + nb;
                 T v[UB];
 #pragma unroll
                 for (int u = 0; u < UB; ++u) v[u] = alpha * acc[i][s * UB + u][r];
