@@ -477,6 +477,20 @@ __host__ __device__ constexpr int slice(int x, int n, int slots)
 {
     return (x + 1) * n / slots - x * n / slots;
 }
+__host__ __device__ constexpr bool slices_cover(int n, int slots)
+{
+    int sum = 0;
+    for (int x = 0; x < slots; ++x) {
+        if (slice(x, n, slots) < 0) return false;
+        sum += slice(x, n, slots);
+    }
+    return sum == n;
+}
+// the regions of the compiled tiles: more MFMAs than memory instructions,
+// fewer, and equal
+static_assert(slices_cover(96, 34) && slices_cover(16, 18) && slices_cover(32, 16) &&
+                  slices_cover(5, 6) && slices_cover(0, 3),
+              "hint slices must add up to the region's MFMAs");
 
 // Scheduling hints for one region of a k step (see gemm_mfma_kernel's
 // step).  hints_a: NLD global loads, NRD fragment reads, then MEM - NLD -
