@@ -87,10 +87,11 @@ def test_cfg4_tall_skinny(cuda):
     del torch
 
 
-def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c, all_rows=False):
+def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c, all_rows=False, ta=0):
     """Full-size GEMM on the GPU; the oracle (accumulating in double) on a
     sample of rows -- or on every row with all_rows -- plus a Freivalds
-    projection of the whole result (C_gpu x vs alpha A (B x) + beta C0 x)."""
+    projection of the whole result (C_gpu x vs alpha op(A) (B x) + beta C0 x).
+    ta=1: A is stored k x m (lda = m) and op(A) is its transpose."""
     import torch
     import sushiblas_amd as sbx
     tdt = torch.float32 if dtype == np.float32 else torch.float64
@@ -107,22 +108,23 @@ def _sampled_rows_check(cuda, dtype, m, n, k, alpha, beta, seed, dist_c, all_row
     A = dA.cpu().numpy()
     B = dB.cpu().numpy()
     C0 = dC.cpu().numpy()
-    sbx.gemm_ex(sbx.F32 if dtype == np.float32 else sbx.F64, 0, 0, 0, m, n, k, alpha, dA, k, 0,
-                dB, n, 0, beta, dC, n, 0)
+    sbx.gemm_ex(sbx.F32 if dtype == np.float32 else sbx.F64, 0, ta, 0, m, n, k, alpha, dA,
+                m if ta else k, 0, dB, n, 0, beta, dC, n, 0)
     torch.cuda.synchronize()
     got = dC.cpu().numpy().reshape(m, n)
+    opA = A.reshape(k, m).T if ta else A.reshape(m, k)
     if all_rows:
         rows = np.arange(m)
     else:
         rows = np.unique(np.concatenate([np.arange(0, 16), np.arange(m - 16, m),
                                          np.random.default_rng(seed).integers(0, m, 32)]))
-    Ar = np.ascontiguousarray(A.reshape(m, k)[rows]).ravel()
+    Ar = np.ascontiguousarray(opA[rows]).ravel()
     Cr = np.ascontiguousarray(C0.reshape(m, n)[rows]).ravel()
     oracle.gemm(0, 0, 0, len(rows), n, k, alpha, Ar, k, B, n, beta, Cr, n, 1)
     err_rows = oracle.rel_fro_err(np.ascontiguousarray(got[rows]), Cr.reshape(len(rows), n))
     x = np.random.default_rng(seed + 7).standard_normal(n)
     lhs = got.astype(np.float64) @ x
-    rhs = alpha * (A.reshape(m, k).astype(np.float64) @ (B.reshape(k, n).astype(np.float64) @ x))
+    rhs = alpha * (opA.astype(np.float64) @ (B.reshape(k, n).astype(np.float64) @ x))
     rhs += beta * (C0.reshape(m, n).astype(np.float64) @ x)
     err_proj = float(np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs))
     print(f"{m}x{n}x{k} {np.dtype(dtype).name}: {len(rows)} rows err={err_rows:.3e} "
@@ -162,6 +164,24 @@ def test_operand_above_2gib(cuda):
     assert name.startswith("mfma_"), name
     e_rows, e_proj = _sampled_rows_check(cuda, np.float32, m, n, k, 1.0, 0.5, SEED + 6,
                                          "uniform")
+    assert e_rows <= TOL[np.float32]
+    assert e_proj <= TOL[np.float32]
+
+
+def test_operand_above_2gib_transposed(cuda):
+    """The same 2.25 GiB A stored transposed (4096 x 147456, lda = 147456):
+    a tile's walk over K then spans more than 2^31 bytes from the tile's
+    origin, so the k loop cannot use its fixed-descriptor section and every
+    k tile goes through the moving descriptors.  Sampled rows against the
+    oracle, plus Freivalds over the whole result."""
+    import sushiblas_amd as sbx
+    m, n, k = 147456, 64, 4096
+    assert m * k * 4 > (2 << 30)
+    name = sbx.gemm_select(sbx.F32, 0, 1, 0, m, n, k, m, n, n)
+    print(f"above-2GiB transposed case {m}x{n}x{k} -> {name}", flush=True)
+    assert name.startswith("mfma_"), name
+    e_rows, e_proj = _sampled_rows_check(cuda, np.float32, m, n, k, 1.0, 0.5, SEED + 7,
+                                         "uniform", ta=1)
     assert e_rows <= TOL[np.float32]
     assert e_proj <= TOL[np.float32]
 
