@@ -45,6 +45,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
 // MFMA shape: 0 = 32x32x2 for fp32 / 16x16x4 for fp64, 1 = 16x16x4 fp32)
 #define SBX_MFMA_CONFIGS(X)  \
     X(float, 256, 256, 32, 4, 2, 1, 2, 0) \
+    X(float, 256, 128, 16, 4, 1, 2, 2, 0) \
     X(float, 128, 128, 16, 2, 2, 2, 2, 0) \
     X(float, 128, 128, 16, 2, 2, 2, 3, 0) \
     X(float, 128, 64, 32, 2, 2, 2, 2, 0) \

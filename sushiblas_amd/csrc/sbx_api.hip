@@ -55,6 +55,7 @@ struct Problem {
 // Tile configurations compiled into the library (gemm_cfg_*.hip).
 enum Cfg {
     F32_256x256,   // large fp32: 8 waves of 64x128, 2 waves/SIMD (128 accumulators)
+    F32_256x128,   // large fp32: 4 waves of 64x128, two workgroups per CU, 2 tiles in flight
     F32_128x128,   // mid-size fp32: 4 waves of 64x64, 2 waves/SIMD, 2 tiles in flight
     F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
@@ -76,7 +77,8 @@ struct CfgInfo {
 };
 
 const CfgInfo kCfg[] = {
-    {"mfma_f32_256x256x32_w4x2", 256, 256, 32, 1}, {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
+    {"mfma_f32_256x256x32_w4x2", 256, 256, 32, 1}, {"mfma_f32_256x128x16_w4x1", 256, 128, 16, 2},
+    {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
     {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
@@ -120,9 +122,21 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
     } else if (m <= 64) {
         out[c++] = wide;
     } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= cus * 3 / 4) {
-        out[c++] = F32_256x256;  // (nearly) full rounds of the largest tile
-        // three 128^2 workgroups per CU beat it where the 256^2 grid ends
-        // in a ragged round or a ragged tile (5000^2 x 1000: 394 vs 450 us)
+        // Large fp32.  Two 256x128 workgroups per CU (64x128 per wave)
+        // overlap each other's prologue and epilogue; they beat the 256^2
+        // tile, which runs alone on its CU, on all 15 shapes timed (8192^3
+        // 7211 vs 7277 us, 12288 x 8192 x 1024 1405 vs 1468 us), so the
+        // 256^2 tile is left to SYRK.  They lead where their grid is (nearly)
+        // whole rounds; elsewhere the 128^2 tile at two per CU, whose finer
+        // grid and split tail land closer to whole rounds, comes first
+        // (5000^2 x 1000: 376 against 422 us, 5120^3: 1786 against 1872 us).
+        const int64_t slots = 2 * cus, left = cdiv(m, 256) * cdiv(n, 128) % slots;
+        const bool whole = left == 0 || left >= slots * 7 / 8;
+        if (whole) out[c++] = F32_256x128;
+        out[c++] = F32_128x128;
+        if (!whole) out[c++] = F32_256x128;
+        // three 128^2 workgroups per CU: one whole round of 4095 x 3001 x
+        // 2047's 768 tiles
         out[c++] = F32_128x128_O3;
     } else {
         out[c++] = sq;
@@ -438,6 +452,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
     switch (cfg) {
     case F32_256x256:
         return launch_mfma<float, 256, 256, 32, 4, 2, 1, 2>(a, akc, bkc, nb, s);
+    case F32_256x128:
+        return launch_mfma<float, 256, 128, 16, 4, 1, 2, 2>(a, akc, bkc, nb, s);
     case F32_128x128:
         return launch_mfma<float, 128, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_128x128_O3:

@@ -83,7 +83,7 @@ def test_noop_cases_need_no_device():
 
 
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,expect", [
-    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x256x32_w4x2"),
+    (0, 0, 0, 0, 8192, 8192, 8192, "mfma_f32_256x128x16_w4x1"),
     (0, 0, 1, 1, 4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),
     (0, 0, 0, 0, 512, 512, 512, "mfma_f32_32x32_ksplit8"),  # one tile per CU, K >= 512
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_256x64x32_w8x1"),
@@ -109,9 +109,10 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
     (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
-    (4096, 4096, 1024, "mfma_f32_256x256x32_w4x2"),
-    (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2_o3+splitk3"),  # 400 ragged 256^2 tiles
-    (6144, 6144, 512, "mfma_f32_128x128x16_w2x2_o3"),           # 576 of 256^2: 2.25 rounds
+    (4096, 4096, 1024, "mfma_f32_256x128x16_w4x1"),       # 512 256x128 tiles: one round at 2 per CU
+    (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2+splitk3"),     # 800 256x128 tiles: 1.56 rounds
+    (6144, 6144, 512, "mfma_f32_128x128x16_w2x2"),              # 4.5 rounds of 128^2
+    (9000, 9000, 3000, "mfma_f32_256x128x16_w4x1"),             # 2556 256x128 tiles: 4.99 rounds
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (128, 1024, 512, "mfma_f32_32x32_ksplit8"),                # 128 tiles, K = 512: 8 waves
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),

@@ -55,7 +55,7 @@ def _fused_case(dev, dtype, layout, ta, tb, m, n, k, alpha, beta, seed, pad=(0, 
 
 
 @pytest.mark.parametrize("dtype,layout,ta,tb,m,n,k,alpha,beta", [
-    (np.float32, 0, 0, 0, 4096, 4096, 64, 1.0, 0.0),      # 256x256 tiles
+    (np.float32, 0, 0, 0, 4096, 4096, 64, 1.0, 0.0),      # 256x128 tiles
     (np.float32, 0, 0, 1, 1000, 777, 300, 1.5, 0.5),       # 128x128 + split-K
     (np.float32, 0, 1, 0, 512, 512, 512, 1.0, 1.0),        # split-K 8
     (np.float32, 0, 0, 0, 8192, 64, 1024, 1.0, -1.0),      # 128x64 tall-skinny

@@ -442,20 +442,23 @@ def test_small_kernel_eight_waves(cuda, ta, tb):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
-# -- the largest fp32 tile on ragged edges ------------------------------------
+# -- the large fp32 tiles on ragged edges --------------------------------------
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_largest_tile_ragged_edges(cuda, ta, tb):
-    """The 256x256 tile (8 waves) with partial tiles on both edges, a K tail
-    (257 = 8*32 + 1) and padded leading dimensions; 4097 x 8191 x 515 adds a
-    split tail.  The ldc padding of C stays untouched."""
+def test_large_tiles_ragged_edges(cuda, ta, tb):
+    """The 256x128 tile (two per CU) with partial tiles on both edges, a K
+    tail (257 = 16*16 + 1) and padded leading dimensions; 4097 x 8191 x 515
+    runs the 128x128 tile with a split tail.  The ldc padding of C stays
+    untouched."""
     import sushiblas_amd as sbx
-    for i, (m, n, k) in enumerate([(8191, 8190, 257), (4097, 8191, 515)]):
+    for i, (m, n, k, want_name) in enumerate([
+            (8191, 8190, 257, "mfma_f32_256x128x16_w4x1"),
+            (4097, 8191, 515, "mfma_f32_128x128x16_w2x2+splitk4")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 80 + i,
                                              pad=(3, 1, 5))
         name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"largest-tile case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name.startswith("mfma_f32_256x256"), name
+        print(f"large-tile case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == want_name, name
         got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
@@ -529,16 +532,17 @@ def test_split_k_is_deterministic(cuda, dtype):
 
 def test_workspace_growth_under_concurrent_host_threads(cuda):
     """Host threads share one (fresh) stream and mix a small split-K shape
-    (workspace within the initial size) with a 256x256-tile shape whose split
+    (workspace within the initial size) with a 128x128-tile shape whose split
     tail needs a larger workspace, so the cache grows while other threads may
     hold the old address.  Every result must match the oracle."""
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 512), (4608, 4096, 512)]
-    # 32 tail tiles of 256x256 cut into >= 5 parts: > 32 MB of partials
-    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4096, 512, 512, 4096, 4096)
-    assert name.startswith("mfma_f32_256x256") and int(name.split("splitk")[1]) >= 5, name
+    shapes = [(512, 512, 512), (4608, 4608, 512)]
+    # 1296 tiles of 128x128: 2 rounds of 512 plus 272 tail tiles, each cut
+    # into >= 3 parts of 64 KiB: > 32 MiB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4608, 512, 512, 4608, 4608)
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 3, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)

@@ -256,6 +256,22 @@ def test_syrk_matches_oracle(cuda, dtype, layout, upper, trans):
             assert _err(got, want) <= TOL[dtype], (n, k)
 
 
+@pytest.mark.parametrize("layout,upper,trans", [(0, 0, 0), (0, 1, 1), (1, 0, 1), (1, 1, 0)])
+def test_syrk_largest_tile_ragged(cuda, layout, upper, trans):
+    """The 256x256 tile (8 waves, one per CU), which only SYRK uses: n = 7553
+    leaves a partial tile on both edges of the triangle, k = 257 a K tail
+    (8*32 + 1), and lda is padded."""
+    import sushiblas_amd as sbx
+    n, k = 7553, 257
+    lda = (n if trans else k) if layout == 0 else (k if trans else n)
+    name = sbx.syrk_select(sbx.F32, layout, upper, trans, n, k, lda + 3, n + 1)
+    print(f"syrk largest-tile case {n}x{k}: {name}", flush=True)
+    assert name == "mfma_f32_256x256x32_w4x2", name
+    got, want, C0 = run_syrk(cuda, np.float32, layout, upper, trans, n, k, 0.5, 1.5, SEED + 60,
+                             pad=(3, 1), sentinel=False)
+    assert _err(got, want) <= TOL[np.float32]
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_syrk_padded_unaligned_batched(cuda, dtype):
     for upper in (0, 1):
