@@ -428,6 +428,24 @@ struct Glob {
 };
 
 // Typed vector store/load of U consecutive C elements (16 bytes for fp32 U=4).
+// U consecutive elements of C one at a time: rows whose address or pitch
+// does not allow vector access.
+template <typename T, int U>
+struct CElems {
+    template <typename P>
+    __device__ static inline void load(const P* p, T* o)
+    {
+#pragma unroll
+        for (int u = 0; u < U; ++u) o[u] = p[u];
+    }
+    template <typename P>
+    __device__ static inline void store(P* p, const T* v)
+    {
+#pragma unroll
+        for (int u = 0; u < U; ++u) p[u] = v[u];
+    }
+};
+
 template <typename T, int U>
 struct CVec {
     template <typename P>
@@ -839,18 +857,20 @@ gemm_mfma_kernel(GemmArgs<T> p)
     }
     const bool read_c = beta != (T)0;
 
-    // A wave tile wholly inside C (and inside the triangle window) with
-    // vector-capable rows -- every split unit and every tile of a large
-    // problem but the edges -- takes a path without per-element tests: a
-    // block row's C loads are all issued before the first of them is used.
-    // (Under the general path's per-element branches each load waited for
-    // its own round trip before the next was issued: ~18 us per round of
-    // 256x256 tiles at 8192^3 with beta != 0.)
-    const bool interior = (UB == 1 || vec_ok) && wm0 + WTM <= row_lim && wn0 + WTN <= col_lim &&
+    // A wave tile wholly inside C (and inside the triangle window) -- every
+    // split unit and every tile of a large problem but the edges -- takes a
+    // path without per-element tests: a block row's C loads are all issued
+    // before the first of them is used.  Rows that allow vector access use
+    // UB-wide loads and stores, others UB single ones.  (Under the general
+    // path's per-element branches each load waited for its own round trip
+    // before the next was issued: ~18 us per round of 256x256 tiles at
+    // 8192^3 with beta != 0.)
+    const bool interior = wm0 + WTM <= row_lim && wn0 + WTN <= col_lim &&
                           wn0 + WTN - 1 <= wm0 + hi_off && wn0 >= wm0 + WTM - 1 + lo_off;
     if (interior) {
         constexpr int NS = NBN / UB;
-        auto finish = [&](auto WITH_C) {
+        auto finish = [&](auto WITH_C, auto VEC) {
+            typedef typename std::conditional<decltype(VEC)::value, CVec<T, UB>, CElems<T, UB>>::type CV;
 #pragma unroll
             for (int i = 0; i < NBM; ++i) {
                 T cv[NS][MF::NACC][UB];
@@ -861,7 +881,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
                         for (int r = 0; r < MF::NACC; ++r) {
                             const int m = wm0 + FragA::map(i, MF::row(r, q));
                             const int nb = wn0 + FragB::map(s * UB, jl);
-                            CVec<T, UB>::load(dst + (int64_t)m * ldd + nb, cv[s][r]);
+                            CV::load(dst + (int64_t)m * ldd + nb, cv[s][r]);
                         }
                 }
 #pragma unroll
@@ -877,12 +897,17 @@ gemm_mfma_kernel(GemmArgs<T> p)
                             if constexpr (decltype(WITH_C)::value) v[u] += beta * cv[s][r][u];
                             if (relu) v[u] = relu_of(v[u]);
                         }
-                        CVec<T, UB>::store(dst + (int64_t)m * ldd + nb, v);
+                        CV::store(dst + (int64_t)m * ldd + nb, v);
                     }
             }
         };
-        if (read_c) finish(Int<1>{});
-        else finish(Int<0>{});
+        if (UB == 1 || vec_ok) {
+            if (read_c) finish(Int<1>{}, std::true_type{});
+            else finish(Int<0>{}, std::true_type{});
+        } else {
+            if (read_c) finish(Int<1>{}, std::false_type{});
+            else finish(Int<0>{}, std::false_type{});
+        }
         return;
     }
 
