@@ -91,9 +91,11 @@ const CfgInfo kCfg[] = {
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Tile configurations worth modelling for a problem, the default first; cus
-// is the device's CU count (the round size of one-per-CU tiles).
-int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out)
+// is the device's CU count (the round size of one-per-CU tiles).  *large is
+// set for the large-fp32 candidates, whose model adds an epilogue term.
+int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out, bool* large)
 {
+    *large = false;
     if (uplo) {
         // a triangle needs square tiles, so diagonal tiles are the tm == tn ones
         if (dtype != SBX_F32) {
@@ -130,6 +132,7 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         // whole rounds; elsewhere the 128^2 tile at two per CU, whose finer
         // grid and split tail land closer to whole rounds, comes first
         // (5000^2 x 1000: 376 against 422 us, 5120^3: 1786 against 1872 us).
+        *large = true;
         const int64_t slots = 2 * cus, left = cdiv(m, 256) * cdiv(n, 128) % slots;
         const bool whole = left == 0 || left >= slots * 7 / 8;
         if (whole) out[c++] = F32_256x128;
@@ -258,9 +261,21 @@ constexpr double kSmallRate = 0.21e12;
 constexpr double kSmallCuRate = 0.31e12;
 constexpr double kSmallF64Rate = 0.7;
 
+// Large fp32 shapes (epi set): a tile's epilogue moves its C tile, and the
+// CU's other workgroups hide only part of that time.  The model adds, per
+// whole tile, kEpiSec per byte of the C tile, times 12 for C rows that take
+// no vector access (single-element loads and stores), and per split part
+// kEpiSec per byte of its partial; both times 0.2 at three workgroups per
+// CU.  Fitted on 78 large shapes (K = 128 ... 8192, beta 0 and 0.5, every
+// large tile and split timed): the pick is within 0.8 % of the fastest on
+// average and 4.1 % at most, against 2.1 % and 30 % without the term
+// (8191 x 8190 x 128: 296 against 229 us).  It does not depend on beta, so
+// sbx_gemm_select names the pick for every beta.
+constexpr double kEpiSec = 0.01e-9;
+
 // max_ws: the most split-partial bytes a plan may use (the allocation-free
 // entry point's scratch size; unlimited otherwise).
-Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws)
+Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi = false)
 {
     if (c == F32_SMALL || c == F64_SMALL) {
         // one launch, no split; the operands' layout hardly matters
@@ -277,8 +292,19 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws)
     const double F = 4e-6, G = 7.5e-6, W = 6e12;
     const double e1 = 0.9;
     const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
-    const double w = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // one whole tile
     const int64_t P = ci.per_cu;
+    double o_tile = 0.0, o_part = 0.0;  // epilogue terms of a whole tile / a split part
+    if (epi) {
+        const int64_t vec_elems = 16 / (int64_t)elem;
+        const bool vec = p.ldc % vec_elems == 0 && ((uintptr_t)p.C % 16) == 0;
+        const double hide = P >= 3 ? 0.2 : 1.0;
+        const double c_bytes = (double)ci.bm * ci.bn * elem;
+        o_tile = kEpiSec * c_bytes * hide * (vec ? 1.0 : 12.0);
+        o_part = kEpiSec * c_bytes * hide;
+    }
+    const double wk = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // a whole tile's MFMA work
+    const double w = wk + o_tile;
+
     const int64_t tiles = tile_count(p, c);
     const int64_t units = tiles * (p.batch > 1 ? p.batch : 1);
     Choice best{c, SplitPlan{(int)tiles, 1, 0}, rounds_time(units, w, P, cus, e1) + F};
@@ -291,7 +317,7 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws)
     for (int64_t sp = 2; sp <= smax; ++sp) {
         if ((size_t)(rem * sp) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
         const double t = rounds_time(full, w, P, cus, e1) +
-                         rounds_time(rem * sp, w / (double)sp, P, cus, e1) + F + G +
+                         rounds_time(rem * sp, wk / (double)sp + o_part, P, cus, e1) + F + G +
                          (double)(rem * sp) * ci.bm * ci.bn * elem / W;
         if (t < best.seconds * 0.98)
             best = Choice{c, SplitPlan{(int)full, (int)sp, (int)rem}, t};
@@ -507,7 +533,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (algo != SBX_ALGO_GENERIC) {
         Cfg cands[5];
         const int64_t cus = cu_count();
-        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands);
+        bool large = false;
+        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
         bool any = false;
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
         for (int i = 0; i < nc; ++i) {
@@ -515,7 +542,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL;
             if (algo == SBX_ALGO_MFMA_TILE && small) continue;
             if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
-            const Choice c = model_plan(p, cands[i], cus, fixed_ws ? fixed_bytes : SIZE_MAX);
+            const Choice c = model_plan(p, cands[i], cus, fixed_ws ? fixed_bytes : SIZE_MAX, large);
             // The 8-wave 256x64 tile off whole rounds only with a split
             // tail: unsplit, its last partial round ran behind 128x64 at
             // two per CU (100000x63x515: 86 against 82 us), which the

@@ -113,6 +113,8 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2+splitk3"),     # 800 256x128 tiles: 1.56 rounds
     (6144, 6144, 512, "mfma_f32_128x128x16_w2x2"),              # 4.5 rounds of 128^2
     (9000, 9000, 3000, "mfma_f32_256x128x16_w4x1"),             # 2556 256x128 tiles: 4.99 rounds
+    (8192, 8192, 257, "mfma_f32_256x128x16_w4x1"),              # short K, vector C rows
+    (8191, 8190, 257, "mfma_f32_128x128x16_w2x2_o3"),           # C rows without vector access
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (128, 1024, 512, "mfma_f32_32x32_ksplit8"),                # 128 tiles, K = 512: 8 waves
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),

@@ -447,15 +447,18 @@ def test_small_kernel_eight_waves(cuda, ta, tb):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_large_tiles_ragged_edges(cuda, ta, tb):
     """The 256x128 tile (two per CU) with partial tiles on both edges, a K
-    tail (257 = 16*16 + 1) and padded leading dimensions; 4097 x 8191 x 515
-    runs the 128x128 tile with a split tail.  The ldc padding of C stays
-    untouched."""
+    tail (257 = 16*16 + 1) and padded leading dimensions.  With ldc = n + 5
+    no C row allows vector access, and the same shape runs the three-per-CU
+    128^2 tile, whose interior tiles then load and store C one element at a
+    time.  4097 x 8191 x 515 runs the 128x128 tile with a split tail.  The
+    ldc padding of C stays untouched."""
     import sushiblas_amd as sbx
-    for i, (m, n, k, want_name) in enumerate([
-            (8191, 8190, 257, "mfma_f32_256x128x16_w4x1"),
-            (4097, 8191, 515, "mfma_f32_128x128x16_w2x2+splitk4")]):
+    for i, (m, n, k, c_pad, want_name) in enumerate([
+            (8191, 8190, 257, 6, "mfma_f32_256x128x16_w4x1"),
+            (8191, 8190, 257, 5, "mfma_f32_128x128x16_w2x2_o3"),
+            (4097, 8191, 515, 5, "mfma_f32_128x128x16_w2x2+splitk4")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 80 + i,
-                                             pad=(3, 1, 5))
+                                             pad=(3, 1, c_pad))
         name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
         print(f"large-tile case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
         assert name == want_name, name
@@ -538,10 +541,10 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 512), (4608, 4608, 512)]
-    # 1296 tiles of 128x128: 2 rounds of 512 plus 272 tail tiles, each cut
-    # into >= 3 parts of 64 KiB: > 32 MiB of partials
-    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 4608, 4608, 512, 512, 4608, 4608)
+    shapes = [(512, 512, 512), (2304, 4864, 1024)]
+    # 18 x 38 = 684 tiles of 128x128: a round of 512 plus 172 tail tiles, each
+    # cut into >= 3 parts of 64 KiB: > 32 MiB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 2304, 4864, 1024, 1024, 4864, 4864)
     assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 3, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
