@@ -957,7 +957,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
 // (and the ReLU when fused); for a triangle, only the triangle's elements.
 // One lane per element, one workgroup of 256 lanes per (slot, 256-element
 // chunk); all of a lane's partial loads are issued before the sum.
-constexpr int kMaxSplitParts = 8;
+constexpr int kMaxSplitParts = 32;
 
 template <typename T, int BM, int BN>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)

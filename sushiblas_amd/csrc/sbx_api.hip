@@ -204,7 +204,8 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     random fp32 shapes from 300 to 7000 per dimension; over all 148
 //     shapes the pick is within 0.7 % of the fastest on average).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
-// may be cut into s <= 8 k-ranges.  A split is taken if predicted >= 2 %
+// may be cut into s <= 32 k-ranges (at least 2 k tiles each; a part costs a
+// fixed kPartSec more).  A split is taken if predicted >= 2 %
 // faster, another tile shape if >= 3 % faster than the default.
 // Split partials live in a workspace cached per (device, stream): calls on
 // one stream are ordered, so they can share it; the first call that needs
@@ -273,6 +274,13 @@ constexpr double kSmallF64Rate = 0.7;
 // sbx_gemm_select names the pick for every beta.
 constexpr double kEpiSec = 0.01e-9;
 
+// Each split part also pays a fixed cost (its pipeline fill and its partial's
+// store).  Fitted on 36 mid-size shapes whose pick splits more than 8 ways
+// and 12 long-K shapes (256^2 x 65536 ...), every split 1-32 of the picked
+// tile timed: the split picked is 0.66 % from that tile's fastest on average
+// and 4.5 % at most (1.3 % and 17 % without the term).
+constexpr double kPartSec = 1e-6;
+
 // max_ws: the most split-partial bytes a plan may use (the allocation-free
 // entry point's scratch size; unlimited otherwise).
 Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi = false)
@@ -317,7 +325,7 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi 
     for (int64_t sp = 2; sp <= smax; ++sp) {
         if ((size_t)(rem * sp) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
         const double t = rounds_time(full, w, P, cus, e1) +
-                         rounds_time(rem * sp, wk / (double)sp + o_part, P, cus, e1) + F + G +
+                         rounds_time(rem * sp, wk / (double)sp + o_part + kPartSec, P, cus, e1) + F + G +
                          (double)(rem * sp) * ci.bm * ci.bn * elem / W;
         if (t < best.seconds * 0.98)
             best = Choice{c, SplitPlan{(int)full, (int)sp, (int)rem}, t};

@@ -108,7 +108,7 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
     (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
-    (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk6"),
+    (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk11"),
     (4096, 4096, 1024, "mfma_f32_256x128x16_w4x1"),       # 512 256x128 tiles: one round at 2 per CU
     (5000, 5000, 1000, "mfma_f32_128x128x16_w2x2+splitk3"),     # 800 256x128 tiles: 1.56 rounds
     (6144, 6144, 512, "mfma_f32_128x128x16_w2x2"),              # 4.5 rounds of 128^2
@@ -118,7 +118,9 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (128, 1024, 512, "mfma_f32_32x32_ksplit8"),                # 128 tiles, K = 512: 8 waves
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
-    (512, 512, 2048, "mfma_f32_64x128x32_w2x2+splitk8"),       # long K: the tile kernel's split
+    (512, 512, 2048, "mfma_f32_32x32_ksplit8"),                # 256 32^2 tiles, K over 8 waves
+    (256, 256, 65536, "mfma_f32_64x128x32_w2x2+splitk32"),     # 8 tiles: a 32-way split fills the CUs
+    (325, 351, 12266, "mfma_f32_64x128x32_w2x2+splitk14"),
 ])
 def test_model_based_selection(m, n, k, expect):
     """Tile shape and split from the cost model (whole rounds unsplit, the
@@ -128,7 +130,7 @@ def test_model_based_selection(m, n, k, expect):
 
 
 @pytest.mark.parametrize("dtype,n,k,expect", [
-    (0, 8192, 8192, "mfma_f32_128x128x16_w2x2_o3+splitk7"),  # 2080 triangle tiles
+    (0, 8192, 8192, "mfma_f32_256x256x32_w4x2+splitk11"),    # 528 triangle tiles of 256^2
     (0, 5000, 5000, "mfma_f32_128x128x16_w2x2_o3+splitk4"),
     (0, 2048, 2048, "mfma_f32_128x128x16_w2x2_o3+splitk5"),
     (1, 8192, 8192, "mfma_f64_128x128x16_w2x2+splitk6"),

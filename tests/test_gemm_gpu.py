@@ -533,6 +533,30 @@ def test_split_k_is_deterministic(cuda, dtype):
     assert normwise(0, g1, want, m, n, ldc) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_long_k_wide_splits(cuda, dtype):
+    """Small outputs over a long K: the tail is cut into up to 32 k-ranges
+    (256 x 256 x 65536: 8 tiles, 32 parts each), and the reduction sums up
+    to 32 partials per element in part order.  Ragged edges, padded leading
+    dimensions and a K tail on the second shape; whole results against the
+    oracle, the ldc padding untouched, two runs bit-identical."""
+    import sushiblas_amd as sbx
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    for i, (m, n, k) in enumerate([(256, 256, 65536), (325, 351, 12266)]):
+        A, lda, B, ldb, C, ldc = make_inputs(dtype, 0, 0, 0, m, n, k, SEED + 74 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(code, 0, 0, 0, m, n, k, lda, ldb, ldc)
+        print(f"long-K case {m}x{n}x{k} {np.dtype(dtype).name} -> {name}", flush=True)
+        assert "+splitk" in name and int(name.split("splitk")[1]) > 8, name
+        g1 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
+        g2 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
+        np.testing.assert_array_equal(g1.view(np.uint8), g2.view(np.uint8))
+        want = run_oracle(0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, g1, want, m, n, ldc) <= TOL[dtype], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(g1[outside], C[outside])
+
+
 def test_workspace_growth_under_concurrent_host_threads(cuda):
     """Host threads share one (fresh) stream and mix a small split-K shape
     (workspace within the initial size) with a 128x128-tile shape whose split
@@ -541,11 +565,11 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 512), (2304, 4864, 1024)]
-    # 18 x 38 = 684 tiles of 128x128: a round of 512 plus 172 tail tiles, each
-    # cut into >= 3 parts of 64 KiB: > 32 MiB of partials
-    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 2304, 4864, 1024, 1024, 4864, 4864)
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 3, name
+    shapes = [(512, 512, 512), (1280, 1664, 2048)]
+    # 10 x 13 = 130 tiles of 128x128, all short of one round, each cut into
+    # >= 5 parts of 64 KiB: > 32 MiB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 1280, 1664, 2048, 2048, 1664, 1664)
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 5, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)
@@ -593,7 +617,7 @@ def test_split_k_per_thread_streams(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 2048), (384, 320, 3000)]
+    shapes = [(1024, 1024, 4096), (384, 320, 3000)]
     data = []
     for i, (m, n, k) in enumerate(shapes):
         name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
@@ -636,7 +660,8 @@ def test_split_k_on_two_streams(cuda):
     streams do not corrupt each other."""
     import torch
     import sushiblas_amd as sbx
-    m, n, k = 512, 512, 2048
+    m, n, k = 1024, 1024, 4096
+    assert "+splitk" in sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 71)
     want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()

@@ -61,19 +61,19 @@ def test_noalloc_matches_gemm_ex_two_calls(cuda, dtype):
 
 
 def test_noalloc_bounds_the_split_to_the_scratch(cuda):
-    """A problem whose preferred split needs more than the scratch (172 tail
-    tiles of 128x128 cut 3+ ways: > 32 MiB of partials) runs with a split
+    """A problem whose preferred split needs more than the scratch (130
+    tiles of 128x128 cut 5+ ways: > 32 MiB of partials) runs with a split
     that fits; the result stays within tolerance of the oracle and of
     sbx_gemm_ex.  A second, smaller call follows."""
     import torch
     import sushiblas_amd as sbx
     stream = torch.cuda.Stream()
-    m, n, k = 2304, 4864, 1024
+    m, n, k = 1280, 1664, 2048
     name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     parts = int(name.split("splitk")[1])
-    # 18 x 38 = 684 tiles: a round of 512 and a tail of 172
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and 172 * parts * 128 * 128 * 4 > SCRATCH, name
-    for i, (mm, nn, kk) in enumerate([(m, n, k), (512, 512, 2048)]):
+    # 10 x 13 = 130 tiles, all short of one round
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and 130 * parts * 128 * 128 * 4 > SCRATCH, name
+    for i, (mm, nn, kk) in enumerate([(m, n, k), (640, 640, 4096)]):
         ref, got, want, ldc = _run_both(cuda, np.float32, mm, nn, kk, 1.0, 0.5, SEED + 10 + i,
                                         stream)
         err = normwise(0, got, want, mm, nn, ldc)
