@@ -392,14 +392,21 @@ std::map<int, std::vector<Workspace*>>* g_ws_pool = new std::map<int, std::vecto
 std::atomic<uint64_t> g_next_thread{1};
 
 // The calling thread's number, and on thread exit the return of the
-// workspaces it keyed through hipStreamPerThread to the pool.  Pooled
-// workspaces keep their buffers and events; their next user waits on the
-// event, which covers work the exited thread left in flight.
+// workspaces it keyed through hipStreamPerThread to the pool.  With the
+// handover ordered only by a device-side wait on the event of the exited
+// thread's last use, a test saw a second thread's partials corrupted: the
+// exited thread's per-thread stream is gone by then.  So the exiting thread
+// first waits for its per-thread stream.  That stream still exists here:
+// acquire touches it before this object is constructed, and thread-local
+// objects are destroyed in reverse order of construction.  A pooled
+// workspace is also handed out only once its event reports complete on the
+// host (until then a new thread gets a new workspace).
 struct ThreadWorkspaces {
     uint64_t id = g_next_thread.fetch_add(1);
     std::vector<WsKey> keys;
     ~ThreadWorkspaces()
     {
+        if (!keys.empty()) (void)hipStreamSynchronize(hipStreamPerThread);
         std::lock_guard<std::mutex> g(g_ws_mutex);
         for (const WsKey& k : keys) {
             auto it = g_ws->find(k);
@@ -427,6 +434,8 @@ struct WorkspaceLease {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess) return false;
         const bool per_thread = s == hipStreamPerThread;
+        // (creates this thread's per-thread stream before t_ws, see above)
+        if (per_thread && hipStreamQuery(s) == hipErrorInvalidHandle) return false;
         const WsKey key{dev, s, per_thread ? t_ws.id : 0};
         Workspace* ws;
         {
@@ -435,13 +444,17 @@ struct WorkspaceLease {
             if (it != g_ws->end()) {
                 ws = it->second;
             } else {
+                // an idle pooled workspace: its last use has completed
                 std::vector<Workspace*>& pool = (*g_ws_pool)[dev];
-                if (!pool.empty()) {
-                    ws = pool.back();
-                    pool.pop_back();
-                } else {
-                    ws = new Workspace();
+                ws = nullptr;
+                for (size_t i = pool.size(); i-- > 0;) {
+                    if (!pool[i]->last || hipEventQuery(pool[i]->last) == hipSuccess) {
+                        ws = pool[i];
+                        pool.erase(pool.begin() + (ptrdiff_t)i);
+                        break;
+                    }
                 }
+                if (!ws) ws = new Workspace();
                 (*g_ws)[key] = ws;
                 if (per_thread) t_ws.keys.push_back(key);
             }

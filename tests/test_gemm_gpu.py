@@ -610,10 +610,13 @@ def test_split_k_per_thread_streams(cuda):
     """hipStreamPerThread names one stream per host thread, so two threads
     issuing split-K GEMMs through it run concurrently on different streams:
     each thread must get its own workspace.  A third and fourth thread start
-    after the first two have exited, without any synchronization, and take
-    their pooled workspaces (the event recorded after the last use orders
-    them after the exited threads' kernels).  Every result must match the
-    oracle."""
+    as soon as the first two have exited, without any synchronization: the
+    pooled workspaces may still be in use, and a thread takes one only once
+    its last use has completed (else a new one).  After a device-wide
+    synchronization a fifth and sixth thread take the (now idle) pooled
+    workspaces.  Threads of the later waves synchronize before they exit,
+    so that their per-thread streams have finished when the results are
+    read.  Every result must match the oracle."""
     import threading
     import torch
     import sushiblas_amd as sbx
@@ -627,29 +630,39 @@ def test_split_k_per_thread_streams(cuda):
         data.append((m, n, k, torch.from_numpy(A).to(cuda), lda, torch.from_numpy(B).to(cuda),
                      ldb, ldc, want))
     outs = {t: [[torch.zeros(d[0] * d[1], device=cuda) for _ in range(4)] for d in data]
-            for t in range(4)}
+            for t in range(6)}
     torch.cuda.synchronize()
     errors = []
 
-    def worker(t):
+    def worker(t, sync_at_exit):
         try:
             for rep in range(4):
                 for j in ((t + rep) % 2, (t + rep + 1) % 2):
                     m, n, k, dA, lda, dB, ldb, ldc, _ = data[j]
                     sbx.sgemm(0, 0, 0, m, n, k, 1.0, dA, lda, dB, ldb, 0.0, outs[t][j][rep], ldc,
                               stream=HIP_STREAM_PER_THREAD)
+            if sync_at_exit:
+                torch.cuda.synchronize()  # from this thread: covers its per-thread stream
         except Exception as e:  # pragma: no cover - reported below
             errors.append(e)
 
-    for wave in ((0, 1), (2, 3)):
-        threads = [threading.Thread(target=worker, args=(t,)) for t in wave]
+    free_before_last = None
+    for wave, sync_at_exit in (((0, 1), False), ((2, 3), True), ((4, 5), True)):
+        if wave[0] == 4:
+            torch.cuda.synchronize()
+            free_before_last = torch.cuda.mem_get_info()[0]
+        threads = [threading.Thread(target=worker, args=(t, sync_at_exit)) for t in wave]
         for th in threads:
             th.start()
         for th in threads:
             th.join()
-    torch.cuda.synchronize()  # waits for every stream, the per-thread ones included
+    torch.cuda.synchronize()
     assert not errors, errors
-    for t in range(4):
+    # the last wave reused idle pooled workspaces (>= 32 MiB each if new); the
+    # runtime's own set-up of two new per-thread streams takes a few MiB
+    grown = free_before_last - torch.cuda.mem_get_info()[0]
+    assert grown < (32 << 20), grown
+    for t in range(6):
         for (m, n, k, _, _, _, _, ldc, want), group in zip(data, outs[t]):
             for o in group:
                 assert normwise(0, o.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32], (t, m)
