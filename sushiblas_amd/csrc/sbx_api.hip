@@ -286,13 +286,24 @@ constexpr double kPartSec = 1e-6;
 Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi = false)
 {
     if (c == F32_SMALL || c == F64_SMALL) {
-        // one launch, no split; the operands' layout hardly matters
+        // One launch, no split.  Its waves read operands straight from
+        // memory in the MFMA lane layout, so a k-contiguous operand is read
+        // as one 16-byte run per row per lane and touches many more cache
+        // lines per load than an x-contiguous one: measured against both
+        // operands x-contiguous on 10 shapes 512^3 .. 1152^3, A and B both
+        // k-contiguous took 1.15-1.29x (fp64 1.26-1.38x), A alone 1.03-1.07x
+        // (fp64 1.04-1.15x), B alone 1.0x (fp64 1.03-1.11x).  The model
+        // charges fp32 only the first (with A alone the tile kernels' picks
+        // were the slower ones: 896^3 27.9 against 23.8 us).
         const double f = c == F64_SMALL ? kSmallF64Rate : 1.0;
+        const bool akc = !p.ta, bkc = p.tb;
+        const double lay = c == F64_SMALL ? (akc && bkc ? 1.3 : akc ? 1.12 : bkc ? 1.07 : 1.0)
+                                          : (akc && bkc ? 1.22 : 1.0);
         const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
         const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
         const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
         const double thr = (double)cdiv(units, cus) * w / (kSmallCuRate * f);
-        const double t = 1.5e-6 + (lat > thr ? lat : thr);
+        const double t = 1.5e-6 + (lat > thr ? lat : thr) * lay;
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];
