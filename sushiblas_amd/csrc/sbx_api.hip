@@ -198,11 +198,12 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 //     W = 6 TB/s;
 //   * the one-launch small-problem kernel (32x32 tiles, work w = 2*32*32*K
 //     each) takes 1.5 us + max(ceil(tiles / 2CUs) * w / Rs, ceil(tiles /
-//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.31 TFLOP/s per CU for fp32
-//     whatever the operand layout, 0.7 of those for fp64 (fitted on 26
-//     more fp32 and 26 more fp64 shapes from 64^3 to 2048x2048x256 and 40
-//     random fp32 shapes from 300 to 7000 per dimension; over all 148
-//     shapes the pick is within 0.7 % of the fastest on average).
+//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.31 TFLOP/s per CU for fp32,
+//     0.7 of those for fp64 (fitted on 26 more fp32 and 26 more fp64
+//     shapes from 64^3 to 2048x2048x256 and 40 random fp32 shapes from 300
+//     to 7000 per dimension; over all 148 shapes the pick is within 0.7 %
+//     of the fastest on average), times a factor for k-contiguous operands
+//     (see model_plan).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
 // may be cut into s <= 32 k-ranges (at least 2 k tiles each; a part costs a
 // fixed kPartSec more).  A split is taken if predicted >= 2 %
