@@ -955,39 +955,76 @@ gemm_mfma_kernel(GemmArgs<T> p)
 // Split-K finish: for tail tile `slot` (tile id num_full + slot), sum the
 // `split` partials in part order (deterministic), then C = alpha*sum + beta*C
 // (and the ReLU when fused); for a triangle, only the triangle's elements.
-// One lane per element, one workgroup of 256 lanes per (slot, 256-element
-// chunk); all of a lane's partial loads are issued before the sum.
+// A lane owns RV consecutive elements of a tile row (16 bytes of each
+// partial); a workgroup of 256 lanes one 256*RV-element chunk of a tail
+// tile.  Partials are read 16 parts at a time, their loads issued before
+// the sums; C is read and written with one vector access where its rows
+// allow.
 constexpr int kMaxSplitParts = 32;
+
+template <typename T, int BM, int BN>
+struct SplitReduce {
+    static constexpr int RV = 16 / (int)sizeof(T);
+    static_assert(BN % RV == 0 && (BM * BN) % (256 * RV) == 0, "tile not divisible over the lanes");
+    static constexpr int CHUNKS = BM * BN / (256 * RV);
+};
 
 template <typename T, int BM, int BN>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
 {
-    constexpr int CHUNKS = BM * BN / 256;
-    const int slot = blockIdx.x / CHUNKS;
-    const int chunk = blockIdx.x - slot * CHUNKS;
+    typedef SplitReduce<T, BM, BN> SR;
+    constexpr int RV = SR::RV;
+    typedef T vec_t __attribute__((ext_vector_type(RV)));
+    typedef typename Glob<vec_t>::type GV;
+    typedef typename Glob<T>::type GT;
+    const int slot = blockIdx.x / SR::CHUNKS;
+    const int chunk = blockIdx.x - slot * SR::CHUNKS;
     int tm, tn;
     tile_coords(p, p.num_full + slot, tm, tn);
-    const int e = chunk * 256 + threadIdx.x;
+    const int e = (chunk * 256 + (int)threadIdx.x) * RV;  // first element, tile-local
     const int m = tm * BM + e / BN;
     const int n = tn * BN + e % BN;
     if (m >= p.M || n >= p.N) return;
-    if ((p.uplo == 1 && n > m) || (p.uplo == 2 && n < m)) return;
-    const T* part0 = p.ws + (int64_t)slot * p.split * (BM * BN) + e;
-    T v[kMaxSplitParts];
+    // columns of this lane's run that C (and the triangle window) keeps
+    int lo = n, hi = min(p.N, n + RV);  // [lo, hi)
+    if (p.uplo == 1) hi = min(hi, m + 1);       // column <= row
+    else if (p.uplo == 2) lo = max(lo, m);      // column >= row
+    if (lo >= hi) return;
+    const GV* part0 = (const GV*)(p.ws + (int64_t)slot * p.split * (BM * BN) + e);
+    constexpr int PV = (BM * BN) / RV;  // vectors per partial
+    vec_t sum = part0[0];
+    for (int q0 = 1; q0 < p.split; q0 += 16) {
+        vec_t v[16];
 #pragma unroll
-    for (int q = 0; q < kMaxSplitParts; ++q) v[q] = q < p.split ? part0[(int64_t)q * (BM * BN)] : (T)0;
-    T sum = v[0];
+        for (int j = 0; j < 16; ++j)
+            if (q0 + j < p.split) v[j] = part0[(int64_t)(q0 + j) * PV];
 #pragma unroll
-    for (int q = 1; q < kMaxSplitParts; ++q)
-        if (q < p.split) sum += v[q];
+        for (int j = 0; j < 16; ++j)
+            if (q0 + j < p.split) sum += v[j];
+    }
     const T* Az;
     const T* Bz;
     T* Cz;
     batch_bases(p, (int64_t)blockIdx.z, Az, Bz, Cz);
-    T* cp = Cz + (int64_t)m * p.ldc + n;
-    T out = p.alpha * sum;
-    if (p.beta != (T)0) out += p.beta * *cp;
-    *cp = p.relu ? relu_of(out) : out;
+    GT* cp = (GT*)(Cz + (int64_t)m * p.ldc + n);
+    const T alpha = p.alpha, beta = p.beta;
+    if (p.c_vec && lo == n && hi == n + RV) {
+        vec_t out = alpha * sum;
+        if (beta != (T)0) out += beta * *(const GV*)cp;
+        if (p.relu) {
+#pragma unroll
+            for (int u = 0; u < RV; ++u) out[u] = relu_of(out[u]);
+        }
+        *(GV*)cp = out;
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < RV; ++u) {
+        if (n + u < lo || n + u >= hi) continue;
+        T out = alpha * sum[u];
+        if (beta != (T)0) out += beta * cp[u];
+        cp[u] = p.relu ? relu_of(out) : out;
+    }
 }
 
 }  // namespace sbx

@@ -35,7 +35,7 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         // the reduction runs 256 threads per block whatever the tile's waves
-        constexpr int CHUNKS = BM * BN / 256;
+        constexpr int CHUNKS = SplitReduce<T, BM, BN>::CHUNKS;
         const dim3 rgrid((unsigned)((tiles - a.num_full) * CHUNKS), 1, (unsigned)batch);
         splitk_reduce_kernel<T, BM, BN><<<rgrid, dim3(256), 0, stream>>>(a);
     }
