@@ -16,15 +16,12 @@
  *   - Launches are asynchronous on `stream` (NULL = the null stream of the
  *     current device; hipStreamPerThread is accepted).  The only allocation
  *     is the workspace for split-K GEMM/SYRK partials and chunked GEMV
- *     partials: cached per (device, stream) -- per (device, host thread) for
- *     hipStreamPerThread, returned to a per-device pool when the thread
- *     exits -- grown with hipMalloc (at least doubling) the first time a
- *     larger one is needed and reused after that; an outgrown buffer is kept,
- *     not freed, until the process ends.  Each use of a workspace waits on an
- *     event recorded after its previous use, so one that changes hands (a
- *     pooled one, or a stream handle reused after hipStreamDestroy) is never
- *     overwritten under kernels still reading it.  If the allocation fails
- *     the call runs without splitting instead of failing.
+ *     partials: cached per (device, stream), grown with hipMalloc (at least
+ *     doubling) the first time a larger one is needed and reused after that;
+ *     an outgrown buffer is kept, not freed, until the process ends.  Uses of
+ *     a workspace are ordered by its stream.  Calls on hipStreamPerThread get
+ *     no workspace and run unsplit.  If the allocation fails the call runs
+ *     without splitting instead of failing.
  *   - Return value is a status code (sbx_status); nothing throws across the
  *     ABI.  The C++ layer turns codes into std::runtime_error, as the
  *     reference's SB_THROW_IF does (include/SushiBLAS/core/logger.hpp:316-323).

@@ -9,7 +9,6 @@
 #include <stdio.h>
 #include <string.h>
 
-#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -365,19 +364,24 @@ int cu_count()
 
 // Split-K partials and chunked-GEMV partials live in a workspace keyed by
 // (device, stream): calls on one stream run in order, so they can share it.
-// hipStreamPerThread names a different stream in every host thread, so for
-// that handle the key is the calling thread instead (a thread number that is
-// never reused), and a thread's workspaces go to a per-device pool when the
-// thread exits.  Every use is ordered after the previous one through an
-// event: the stream waits on the event recorded after the workspace's last
-// use before its kernels are enqueued, so a workspace that passes to another
-// stream -- a pooled one, or a stream handle that the runtime hands out again
-// after hipStreamDestroy -- is never written while older kernels may still
-// read it.
+// A stream handle is the address of the runtime's stream object, which is
+// released only once the device has finished the stream's work (measured:
+// hipStreamDestroy with a 68 ms kernel queued returned after 68 ms, and the
+// next hipStreamCreate returned the same handle), so a handle handed out
+// again finds the old kernels done.
+//
+// hipStreamPerThread gets no workspace: its calls run unsplit.  That handle
+// names a different stream in every host thread, so its workspace would be
+// the calling thread's and would change hands when the thread exits, during
+// the runtime's teardown of the thread's stream.  Two such designs failed:
+// ordering the handover by an event recorded on the exited thread's stream
+// made the runtime report hipErrorCapturedEvent (no capture was active), and
+// with the exiting thread synchronizing its stream instead, a test of six
+// threads in three waves, run repeatedly in one process, aborted with
+// "free(): invalid pointer" on its third run; the cause was not found.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
-    hipEvent_t last = nullptr;  // recorded after the latest use
     // Held from handing out the workspace until the calls that use it are
     // enqueued: a split GEMM (or chunked GEMV) is two kernels, and another
     // host thread's call on the same stream must not land between them and
@@ -388,121 +392,68 @@ struct Workspace {
 struct WsKey {
     int dev;
     hipStream_t stream;
-    uint64_t thread;  // calling thread for hipStreamPerThread, else 0
     bool operator<(const WsKey& o) const
     {
         if (dev != o.dev) return dev < o.dev;
-        if (stream != o.stream) return stream < o.stream;
-        return thread < o.thread;
+        return stream < o.stream;
     }
 };
 
 std::mutex g_ws_mutex;
 // never destroyed: freeing device memory during process teardown is unsafe
 std::map<WsKey, Workspace*>* g_ws = new std::map<WsKey, Workspace*>();
-std::map<int, std::vector<Workspace*>>* g_ws_pool = new std::map<int, std::vector<Workspace*>>();
-std::atomic<uint64_t> g_next_thread{1};
 
-// The calling thread's number, and on thread exit the return of the
-// workspaces it keyed through hipStreamPerThread to the pool.  With the
-// handover ordered only by a device-side wait on the event of the exited
-// thread's last use, a test saw a second thread's partials corrupted: the
-// exited thread's per-thread stream is gone by then.  So the exiting thread
-// first waits for its per-thread stream.  That stream still exists here:
-// acquire touches it before this object is constructed, and thread-local
-// objects are destroyed in reverse order of construction.  A pooled
-// workspace is also handed out only once its event reports complete on the
-// host (until then a new thread gets a new workspace).
-struct ThreadWorkspaces {
-    uint64_t id = g_next_thread.fetch_add(1);
-    std::vector<WsKey> keys;
-    ~ThreadWorkspaces()
-    {
-        if (!keys.empty()) (void)hipStreamSynchronize(hipStreamPerThread);
-        std::lock_guard<std::mutex> g(g_ws_mutex);
-        for (const WsKey& k : keys) {
-            auto it = g_ws->find(k);
-            if (it == g_ws->end()) continue;
-            (*g_ws_pool)[k.dev].push_back(it->second);
-            g_ws->erase(it);
-        }
-    }
-};
-thread_local ThreadWorkspaces t_ws;
-
-// A workspace of at least `bytes` for the calling thread's `stream`, locked
-// for the caller's launches until release (ptr null if it cannot be
-// allocated).  A workspace that is outgrown is retired, not freed: kernels
-// enqueued earlier may not have run yet.  Growth at least doubles, so the
-// retired buffers add up to less than the live one.
+// A workspace of at least `bytes` for `stream`, locked for the caller's
+// launches until release (ptr null if there is none: hipStreamPerThread, or
+// the allocation failed).  A workspace that is outgrown is retired, not
+// freed: kernels enqueued earlier may not have run yet.  Growth at least
+// doubles, so the retired buffers add up to less than the live one.  A
+// failed runtime call here leaves its error as the thread's last error,
+// which the launch check after the caller's kernels would report: since the
+// caller handles the failure (it runs unsplit), that error is consumed.
 struct WorkspaceLease {
     void* ptr = nullptr;
-    Workspace* w = nullptr;
-    hipStream_t stream = nullptr;
     std::unique_lock<std::mutex> lock;
 
     bool acquire(hipStream_t s, size_t bytes)
     {
+        if (s == hipStreamPerThread) return false;
         int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return false;
-        const bool per_thread = s == hipStreamPerThread;
-        // (creates this thread's per-thread stream before t_ws, see above)
-        if (per_thread && hipStreamQuery(s) == hipErrorInvalidHandle) return false;
-        const WsKey key{dev, s, per_thread ? t_ws.id : 0};
+        if (hipGetDevice(&dev) != hipSuccess) return failed();
+        const WsKey key{dev, s};
         Workspace* ws;
         {
             std::lock_guard<std::mutex> g(g_ws_mutex);
-            auto it = g_ws->find(key);
-            if (it != g_ws->end()) {
-                ws = it->second;
-            } else {
-                // an idle pooled workspace: its last use has completed
-                std::vector<Workspace*>& pool = (*g_ws_pool)[dev];
-                ws = nullptr;
-                for (size_t i = pool.size(); i-- > 0;) {
-                    if (!pool[i]->last || hipEventQuery(pool[i]->last) == hipSuccess) {
-                        ws = pool[i];
-                        pool.erase(pool.begin() + (ptrdiff_t)i);
-                        break;
-                    }
-                }
-                if (!ws) ws = new Workspace();
-                (*g_ws)[key] = ws;
-                if (per_thread) t_ws.keys.push_back(key);
-            }
+            Workspace*& slot = (*g_ws)[key];
+            if (!slot) slot = new Workspace();
+            ws = slot;
         }
         lock = std::unique_lock<std::mutex>(ws->launch_mu);
-        if (!ws->last && hipEventCreateWithFlags(&ws->last, hipEventDisableTiming) != hipSuccess) {
-            ws->last = nullptr;
-            return false;
-        }
         if (ws->bytes < bytes) {
             size_t nb = bytes < ((size_t)32 << 20) ? ((size_t)32 << 20) : bytes;
             if (nb < 2 * ws->bytes) nb = 2 * ws->bytes;
             void* p = nullptr;
-            if (hipMalloc(&p, nb) != hipSuccess) return false;  // the old buffer stays
+            if (hipMalloc(&p, nb) != hipSuccess) return failed();  // the old buffer stays
             ws->base = p;
             ws->bytes = nb;
         }
-        // order this use after the previous one, whichever stream made it
-        if (hipStreamWaitEvent(s, ws->last, 0) != hipSuccess) return false;
-        w = ws;
-        stream = s;
         ptr = ws->base;
         return true;
     }
 
-    // Record the end of this use (after the caller's launches), then let the
-    // next caller in.
-    hipError_t release()
+    bool failed()
     {
-        hipError_t e = hipSuccess;
-        if (w) e = hipEventRecord(w->last, stream);
-        w = nullptr;
-        if (lock.owns_lock()) lock.unlock();
-        return e;
+        (void)hipGetLastError();
+        release();
+        return false;
     }
-    ~WorkspaceLease() { (void)release(); }
+
+    // Let the next caller in (after the caller's launches are enqueued).
+    void release()
+    {
+        if (lock.owns_lock()) lock.unlock();
+    }
+    ~WorkspaceLease() { release(); }
 };
 
 hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Problem& p,
@@ -566,6 +517,8 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (algo != SBX_ALGO_GENERIC) {
         Cfg cands[5];
         const int64_t cus = cu_count();
+        // no workspace for hipStreamPerThread: plan unsplit
+        const size_t max_ws = fixed_ws ? fixed_bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
         bool large = false;
         const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
         bool any = false;
@@ -575,7 +528,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL;
             if (algo == SBX_ALGO_MFMA_TILE && small) continue;
             if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
-            const Choice c = model_plan(p, cands[i], cus, fixed_ws ? fixed_bytes : SIZE_MAX, large);
+            const Choice c = model_plan(p, cands[i], cus, max_ws, large);
             // The 8-wave 256x64 tile off whole rounds only with a split
             // tail: unsplit, its last partial round ran behind 128x64 at
             // two per CU (100000x63x515: 86 against 82 us), which the
@@ -660,7 +613,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         }
         if (e != hipSuccess) return SBX_HIP_ERROR;
     }
-    return lease.release() == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
+    return SBX_OK;
 }
 
 int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
@@ -857,7 +810,7 @@ int gemv_run(hipStream_t stream, bool trans, int64_t rows, int64_t cols, T alpha
         }
     }
     if (launch_gemv<T>(a, pl, stream) != hipSuccess) return SBX_HIP_ERROR;
-    return lease.release() == hipSuccess ? SBX_OK : SBX_HIP_ERROR;
+    return SBX_OK;
 }
 
 int gemv_impl(void* stream, int dtype, int layout, int trans, int64_t m, int64_t n,
