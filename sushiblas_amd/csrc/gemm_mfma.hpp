@@ -115,6 +115,10 @@ struct Mfma<double, 0> {
     __device__ static inline int row(int r, int q) { return q + 4 * r; }
 };
 
+// Cache-policy operand of a buffer load with the non-temporal (nt) bit set:
+// the lines it brings in are the first to be evicted, for data read once.
+constexpr int kNonTemporal = 2;
+
 // Raw 16-byte buffer load.  The byte offset need only be 4-byte aligned:
 // gfx950 serves unaligned multi-dword buffer loads (the device runs in
 // unaligned access mode), and range-checks each dword on its own, so a load
@@ -204,6 +208,9 @@ struct GemmArgs {
     // instead of base + z * stride.  Null: strided.
     const void* const* table;
     int table_swap;
+    // Host side only: which operand the launch loads non-temporally (0
+    // none, 1 A, 2 B), picking the kernel's STREAM variant.
+    int stream_op;
 };
 
 // Operand and result bases of batch entry z.
@@ -284,8 +291,9 @@ __device__ inline T relu_of(T x)
 //   KC: the operand's k index is contiguous in memory (tile [X][BK+PAD]).
 //   X : tile extent along m (for A) or n (for B).
 //   KTAIL: K is not a multiple of VEC, so a k-contiguous vector may straddle K.
+//   CPOL: cache-policy bits of the buffer loads (kNonTemporal or 0).
 // ---------------------------------------------------------------------------
-template <typename T, int X, int BK, bool KC, int PF, bool KTAIL, int NTHR = 256>
+template <typename T, int X, int BK, bool KC, int PF, bool KTAIL, int NTHR = 256, int CPOL = 0>
 struct Operand {
     static constexpr int V = 16 / (int)sizeof(T);
     static constexpr int VEC = V;  // elements per global load
@@ -335,7 +343,7 @@ struct Operand {
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             stage[S][j] = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, xok(j) ? off0 + j * off_step : kOobOffset, soff, 0);
+                rs, xok(j) ? off0 + j * off_step : kOobOffset, soff, CPOL);
         krem[S] = k_rem;
     }
 
@@ -345,7 +353,8 @@ struct Operand {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             bool ok = xok(j) && kidx(j) < k_rem;
-            stage[S][j] = raw_load16(rs, ok ? off0 + j * off_step : kOobOffset);
+            stage[S][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, ok ? off0 + j * off_step : kOobOffset, 0, CPOL);
         }
         krem[S] = k_rem;
     }
@@ -560,8 +569,9 @@ __device__ inline void hints_b()
 // one is multiplied; 2 = the one after that too, for HBM-bound shapes).
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
 // MI: MFMA shape (see Mfma; fp32 only has a choice).
+// STREAM: the operand whose loads are non-temporal (0 none, 1 A, 2 B).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          bool KTAIL, int PF, int WPE, int MI = 0>
+          bool KTAIL, int PF, int WPE, int MI = 0, int STREAM = 0>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
@@ -576,8 +586,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
     static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");
     static_assert(BK % KG == 0, "BK must be a multiple of the k group");
     static_assert(PF >= 1 && PF <= 4, "prefetch depth 1 to 4");
-    typedef Operand<T, BM, BK, A_KC, PF, KTAIL, NTHR> OpA;
-    typedef Operand<T, BN, BK, B_KC, PF, KTAIL, NTHR> OpB;
+    typedef Operand<T, BM, BK, A_KC, PF, KTAIL, NTHR, STREAM == 1 ? kNonTemporal : 0> OpA;
+    typedef Operand<T, BN, BK, B_KC, PF, KTAIL, NTHR, STREAM == 2 ? kNonTemporal : 0> OpB;
     typedef Frag<T, NBM, A_KC, OpA::LD, MI> FragA;
     typedef Frag<T, NBN, B_KC, OpB::LD, MI> FragB;
 

@@ -504,6 +504,32 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Pr
     }
 }
 
+// The operand whose loads go non-temporal (0 none, 1 A, 2 B).  A grid one
+// tile column wide reads each element of A exactly once (one tile row: B).
+// When that operand is also larger than the 256 MB last-level cache, no
+// cache can keep it from one call to the next, and loading it non-temporal
+// leaves the caches to the other operand: 65536 x 64 x 4096 281-283 ->
+// 270-271 us, 70000 x 64 x 4096 +2 %, 64 x 65536 x 4096 +1-2 % (bit-identical).
+// A smaller one is left alone: repeated calls then find it in that cache
+// (100000 x 63 x 515, 206 MB: 9-13 % slower non-temporal).
+constexpr int64_t kStreamBytes = (int64_t)256 << 20;
+int stream_operand(const Problem& p, int tiles_m, int tiles_n)
+{
+    const int64_t elem = p.dtype == SBX_F32 ? 4 : 8;
+    const int64_t copies = p.batch > 1 ? p.batch : 1;
+    if (tiles_n == 1) {
+        const int64_t rows = p.ta ? p.k : p.m, cols = p.ta ? p.m : p.k;
+        const int64_t per = ((rows - 1) * p.lda + cols) * elem;
+        if ((p.str_a || p.table ? copies : 1) * per > kStreamBytes) return 1;
+    }
+    if (tiles_m == 1) {
+        const int64_t rows = p.tb ? p.n : p.k, cols = p.tb ? p.k : p.n;
+        const int64_t per = ((rows - 1) * p.ldb + cols) * elem;
+        if ((p.str_b || p.table ? copies : 1) * per > kStreamBytes) return 2;
+    }
+    return 0;
+}
+
 // fixed_ws / fixed_bytes: caller-provided split workspace (the
 // allocation-free entry point's scratch); null: the stream's cached one.
 template <typename T>
@@ -608,6 +634,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.tiles = (int)tiles;
             a.table = p.table ? p.table + 3 * b0 : nullptr;
             a.table_swap = p.table_swap;
+            a.stream_op = stream_operand(p, a.tiles_m, a.tiles_n);
             // A (m x k) is k-contiguous iff not transposed, B (k x n) iff transposed
             e = launch_cfg(cfg, a, !p.ta, p.tb != 0, p, nb, stream);
         }

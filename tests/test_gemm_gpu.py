@@ -515,6 +515,27 @@ def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
+@pytest.mark.parametrize("dtype,m,n,k,ta,tb,kernel", [
+    (np.float32, 48, 70000, 1024, 0, 0, "mfma_f32_64x128x32_w2x2+splitk"),  # B 287 MB
+    (np.float32, 48, 70000, 1024, 1, 1, "mfma_f32_64x128x32_w2x2+splitk"),
+    (np.float32, 64, 65536, 1024, 0, 1, "mfma_f32_64x128x32_w2x2"),         # B 268 MB
+    (np.float64, 65536, 64, 1024, 0, 0, "mfma_f64_128x64x16_w2x2"),         # A 537 MB
+    (np.float64, 65536, 40, 1024, 1, 0, "mfma_f64_128x64x16_w2x2"),
+    (np.float32, 70000, 64, 4096, 1, 0, "mfma_f32_256x64x32_w8x1+splitk"),  # A 1.15 GB
+])
+def test_streamed_operand_above_last_level_cache(cuda, dtype, m, n, k, ta, tb, kernel):
+    """A grid one tile wide reads its long operand once; above 256 MiB that
+    operand's loads are non-temporal (a kernel variant with the nt cache
+    policy, unsplit and with a split tail).  Every output against the oracle."""
+    import sushiblas_amd as sbx
+    lda, ldb = (m if ta else k), (k if tb else n)
+    name = sbx.gemm_select(sbx.F32 if dtype == np.float32 else sbx.F64, 0, ta, tb, m, n, k,
+                           lda, ldb, n)
+    assert name.startswith(kernel), name
+    err, _, _ = _case(cuda, dtype, 0, ta, tb, m, n, k, 1.0, 0.5, SEED + 83)
+    assert err <= TOL[dtype]
+
+
 # -- split-K of under-filled grids ---------------------------------------------
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
