@@ -508,10 +508,11 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Pr
 // tile column wide reads each element of A exactly once (one tile row: B).
 // When that operand is also larger than the 256 MB last-level cache, no
 // cache can keep it from one call to the next, and loading it non-temporal
-// leaves the caches to the other operand: 65536 x 64 x 4096 281-283 ->
-// 270-271 us, 70000 x 64 x 4096 +2 %, 64 x 65536 x 4096 +1-2 % (bit-identical).
-// A smaller one is left alone: repeated calls then find it in that cache
-// (100000 x 63 x 515, 206 MB: 9-13 % slower non-temporal).
+// leaves the caches to the other operand (bit-identical; interleaved
+// timings): 65536 x 64 x 4096 (1 GiB) 271.0-271.8 -> 265.1-265.7 us,
+// 131072 x 48 x 1024 (512 MiB) +2.4-4.4 %.  A smaller one keeps the default
+// policy, so repeated calls find it in that cache (100000 x 63 x 515,
+// 206 MB: 9 % slower non-temporal).
 constexpr int64_t kStreamBytes = (int64_t)256 << 20;
 int stream_operand(const Problem& p, int tiles_m, int tiles_n)
 {
