@@ -17,9 +17,9 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
     // K that is not a multiple of the 16-byte vector (it costs 1-4 %)
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
     // A grid one tile wide reads its operand once (see run() for when that
-    // operand's loads go non-temporal); only the tall (BN == 64) and wide
-    // (BM == 64) tiles, whose grids are that, compile the streaming form.
-    constexpr int kStream = BN == 64 ? 1 : (BM == 64 ? 2 : 0);
+    // operand's loads go non-temporal); only the tall (BN <= 64) and wide
+    // (BM <= 64) tiles, whose grids are that, compile the streaming form.
+    constexpr int kStream = BN <= 64 ? 1 : (BM <= 64 ? 2 : 0);
     const bool streamed = kStream != 0 && a.stream_op == kStream;
 #define SBX_LAUNCH(AK, BKC, TAIL)                                                                 \
     do {                                                                                          \

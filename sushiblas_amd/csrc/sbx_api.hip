@@ -60,6 +60,9 @@ enum Cfg {
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
     F32_256x64,    // n <= 64 with a full round of 256-row tiles: 8 waves of 32x64 (16x16x4 MFMAs)
     F32_64x128,    // m <= 64
+    F32_64x256,    // m <= 64 with a full round of 256-column tiles: 8 waves of 64x32 (16x16x4 MFMAs)
+    F32_128x32,    // n <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
+    F32_32x128,    // m <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
     F64_64x128,
@@ -80,7 +83,8 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
-    {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},
+    {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},   {"mfma_f32_64x256x32_w1x8", 64, 256, 32, 1},
+    {"mfma_f32_128x32x32_w4x1", 128, 32, 32, 2},   {"mfma_f32_32x128x32_w1x4", 32, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
     {"mfma_f64_32x32_ksplit4", 32, 32, 32, 1},     {"mfma_f32_32x32_ksplit8", 32, 32, 32, 1},
@@ -116,11 +120,19 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
     const Cfg wide = f32 ? F32_64x128 : F64_64x128;   // m <= 64
     int c = 0;
     if (n <= 64) {
+        // n <= 32: a 64-wide tile would spend half its MFMAs on padding,
+        // where a 32-wide one streams A at up to 5.9 TB/s (65536 x 32 x
+        // 4096: 183 against 272 us; 40000 x 32 x 2048: 76 against 85 us)
+        if (f32 && n <= 32) out[c++] = F32_128x32;
         // one 8-wave 256-row workgroup per CU: B is read by half as many
         // workgroups (65536 x 64 x 4096: 291-294 us against 296-300)
         if (f32 && cdiv(m, 256) >= cus) out[c++] = F32_256x64;
         out[c++] = tall;
     } else if (m <= 64) {
+        // the mirror of the tall case (column-major tall-skinny calls land
+        // here): 64 x 65536 x 4096 270-272 against 280-284 us for 64x128
+        if (f32 && m <= 32) out[c++] = F32_32x128;  // (32 x 65536 x 4096: 166 against 245 us)
+        if (f32 && cdiv(n, 256) >= cus) out[c++] = F32_64x256;
         out[c++] = wide;
     } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= cus * 3 / 4) {
         // Large fp32.  Two 256x128 workgroups per CU (64x128 per wave)
@@ -261,6 +273,11 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
 constexpr double kSmallRate = 0.21e12;
 constexpr double kSmallCuRate = 0.31e12;
 constexpr double kSmallF64Rate = 0.7;
+// Its operand bytes at kSmallBw bound it too: a long reduction over a wide
+// operand streams (32 x 65536 x 4096: 283 us measured, 218 from the rates
+// alone -- 1.07 GB at 3.8 TB/s -- and 241 for the 64x256 tile).  The shapes
+// the rates were fitted on move too few bytes for this to bind.
+constexpr double kSmallBw = 4e12;
 
 // Large fp32 shapes (epi set): a tile's epilogue moves its C tile, and the
 // CU's other workgroups hide only part of that time.  The model adds, per
@@ -303,7 +320,11 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi 
         const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
         const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
         const double thr = (double)cdiv(units, cus) * w / (kSmallCuRate * f);
-        const double t = 1.5e-6 + (lat > thr ? lat : thr) * lay;
+        const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
+        const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
+                             (double)(p.batch > 1 ? p.batch : 1);
+        const double compute = (lat > thr ? lat : thr) * lay;
+        const double t = 1.5e-6 + (compute > bytes / kSmallBw ? compute : bytes / kSmallBw);
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];
@@ -474,6 +495,12 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2, 1>(a, akc, bkc, nb, s);
     case F32_64x128:
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
+    case F32_64x256:
+        return launch_mfma<float, 64, 256, 32, 1, 8, 2, 2, 1>(a, akc, bkc, nb, s);
+    case F32_128x32:
+        return launch_mfma<float, 128, 32, 32, 4, 1, 2, 2, 1>(a, akc, bkc, nb, s);
+    case F32_32x128:
+        return launch_mfma<float, 32, 128, 32, 1, 4, 2, 2, 1>(a, akc, bkc, nb, s);
     case F32_SMALL:
         return launch_small(a, akc, bkc, nb, s, 4);
     case F32_SMALL8:
@@ -560,10 +587,13 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             // tail: unsplit, its last partial round ran behind 128x64 at
             // two per CU (100000x63x515: 86 against 82 us), which the
             // model rates alike; with a split tail it won (80000x64x2048
-            // +splitk4: 195 against 210 us unsplit 128x64).
-            if (cands[i] == F32_256x64 && c.sp.split == 1 &&
-                tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1) % cus != 0)
-                continue;
+            // +splitk4: 195 against 210 us unsplit 128x64).  Its 64x256
+            // mirror only on whole rounds: off them the 64x128 tile with a
+            // split tail was 2-4 % faster than it, split or not
+            // (48x100000x1024, 64x70000x2048, 64x80000x2048).
+            const bool whole = tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1) % cus == 0;
+            if (cands[i] == F32_256x64 && c.sp.split == 1 && !whole) continue;
+            if (cands[i] == F32_64x256 && !whole) continue;
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
             any = true;
         }

@@ -89,6 +89,12 @@ def test_noop_cases_need_no_device():
     (0, 0, 0, 0, 65536, 64, 4096, "mfma_f32_256x64x32_w8x1"),
     (0, 0, 0, 0, 37, 1000, 300, "mfma_f32_32x32_ksplit4"),
     (0, 1, 0, 0, 64, 65536, 4096, "mfma_f32_256x64x32_w8x1"),
+    (0, 0, 0, 0, 64, 65536, 4096, "mfma_f32_64x256x32_w1x8"),
+    (0, 1, 0, 0, 65536, 64, 4096, "mfma_f32_64x256x32_w1x8"),  # column-major tall-skinny
+    (0, 0, 0, 0, 32, 65536, 4096, "mfma_f32_32x128x32_w1x4"),  # m <= 32: 32-row tiles
+    (0, 0, 0, 0, 65536, 32, 4096, "mfma_f32_128x32x32_w4x1"),  # n <= 32: 32-column tiles
+    (0, 0, 0, 0, 48, 65536, 4096, "mfma_f32_64x256x32_w1x8"),  # the small kernel would stream B
+    (0, 0, 0, 0, 64, 80000, 2048, "mfma_f32_64x128x32_w2x2+splitk2"),  # 64x256 off whole rounds
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
 ])

@@ -490,6 +490,64 @@ def test_tall_skinny_eight_wave_tile(cuda, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_wide_eight_wave_tile(cuda, ta, tb):
+    """The 8-wave 64x256 tile, the tall tile's mirror (m <= 64 with a full
+    round of 256-column tiles): a ragged last column tile, m = 63 and a K
+    tail (515); 64 x 65536 x 1100, whose B (288 MB) is loaded
+    non-temporal; m = 48.  Padded leading dimensions; the ldc padding of C
+    stays untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k) in enumerate([(63, 65535, 515), (64, 65536, 1100), (48, 65536, 2048)]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 84 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"wide case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == "mfma_f32_64x256x32_w1x8", name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_narrow_tiles(cuda, ta, tb):
+    """The 32-wide tiles (128x32 for n <= 32, its 32x128 mirror for m <= 32):
+    ragged last tiles with a K tail (515); a split tail (40000 x 32 x 2048,
+    3 parts); an operand above 256 MiB loaded non-temporal (1100 deep);
+    n = 1.  Padded leading dimensions; the ldc padding of C stays untouched."""
+    import sushiblas_amd as sbx
+    cases = [(65535, 31, 515, "mfma_f32_128x32x32_w4x1"),
+             (40000, 32, 2048, "mfma_f32_128x32x32_w4x1+splitk3"),
+             (65536, 32, 1100, "mfma_f32_128x32x32_w4x1"),
+             (4096, 1, 4096, "mfma_f32_128x32x32_w4x1+splitk8"),
+             (31, 65535, 515, "mfma_f32_32x128x32_w1x4"),
+             (32, 65536, 1100, "mfma_f32_32x128x32_w1x4")]
+    for i, (m, n, k, want_name) in enumerate(cases):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 100 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"narrow case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == want_name, name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.5, A, lda, B, ldb, 1.5, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, -0.5, A, lda, B, ldb, 1.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
+def test_column_major_tall_skinny(cuda):
+    """cfg4's shape (65536 x 64 x 4096) in column-major storage: C^T = B^T A^T
+    makes it the wide row-major problem 64 x 65536 x 4096, which runs on the
+    64x256 tile with the long operand loaded non-temporal."""
+    import sushiblas_amd as sbx
+    m, n, k = 65536, 64, 4096
+    assert sbx.gemm_select(sbx.F32, 1, 0, 0, m, n, k, m, k, m) == "mfma_f32_64x256x32_w1x8"
+    err, _, _ = _case(cuda, np.float32, 1, 0, 0, m, n, k, 1.0, 0.0, SEED + 87)
+    assert err <= TOL[np.float32]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
     """The 8-wave 256x64 tile where its grid is not one whole round:
     80000 x 64 x 2048 runs 256 whole tiles plus a 57-tile tail cut 4 ways
@@ -518,7 +576,7 @@ def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
 @pytest.mark.parametrize("dtype,m,n,k,ta,tb,kernel", [
     (np.float32, 48, 70000, 1024, 0, 0, "mfma_f32_64x128x32_w2x2+splitk"),  # B 287 MB
     (np.float32, 48, 70000, 1024, 1, 1, "mfma_f32_64x128x32_w2x2+splitk"),
-    (np.float32, 64, 65536, 1024, 0, 1, "mfma_f32_64x128x32_w2x2"),         # B 268 MB
+    (np.float32, 64, 65536, 1024, 0, 1, "mfma_f32_64x256x32_w1x8"),         # B 268 MB
     (np.float64, 65536, 64, 1024, 0, 0, "mfma_f64_128x64x16_w2x2"),         # A 537 MB
     (np.float64, 65536, 40, 1024, 1, 0, "mfma_f64_128x64x16_w2x2"),
     (np.float32, 70000, 64, 4096, 1, 0, "mfma_f32_256x64x32_w8x1+splitk"),  # A 1.15 GB
