@@ -56,7 +56,8 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
     X(float, 32, 128, 32, 1, 4, 2, 2, 1) \
     X(double, 128, 128, 16, 2, 2, 1, 2, 0) \
     X(double, 128, 64, 16, 2, 2, 2, 2, 0) \
-    X(double, 64, 128, 16, 2, 2, 2, 2, 0)
+    X(double, 64, 128, 16, 2, 2, 2, 2, 0) \
+    X(double, 64, 64, 16, 2, 2, 2, 2, 0)
 
 #define SBX_EXTERN_LAUNCH(T, BM, BN, BK, WM, WN, PF, WPE, MI)                                    \
     extern template hipError_t launch_mfma<T, BM, BN, BK, WM, WN, PF, WPE, MI>(                     \

@@ -66,6 +66,7 @@ enum Cfg {
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
     F64_64x128,
+    F64_64x64,     // fp64 mid-size: 4 waves of 32x32
     F32_SMALL,     // small problems: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
     F64_SMALL,
     F32_SMALL8,    // the same with 8 waves: at most one tile per CU and K >= 512
@@ -86,10 +87,12 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},   {"mfma_f32_64x256x32_w1x8", 64, 256, 32, 1},
     {"mfma_f32_128x32x32_w4x1", 128, 32, 32, 2},   {"mfma_f32_32x128x32_w1x4", 32, 128, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
-    {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
+    {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f64_64x64x16_w2x2", 64, 64, 16, 2},
+    {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
     {"mfma_f64_32x32_ksplit4", 32, 32, 32, 1},     {"mfma_f32_32x32_ksplit8", 32, 32, 32, 1},
     {"generic_64x64x16", 64, 64, 16, 4},
 };
+static_assert(sizeof(kCfg) / sizeof(kCfg[0]) == GENERIC + 1, "one kCfg entry per Cfg, in order");
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -155,6 +158,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
     } else {
         out[c++] = sq;
         if (f32) out[c++] = F32_128x128_O3;
+        // fp64 mid-size: four 64^2 tiles per 128^2 (1024^3 NN 36 against
+        // 52 us on the small-problem kernel; 1536^3 +splitk4 107 against
+        // 137 us for 128^2 +splitk3)
+        if (!f32) out[c++] = F64_64x64;
         // the two 64-wide tiles model alike; measured, 64x128 is the faster
         // one on most square-ish shapes, so it comes first
         out[c++] = wide;
@@ -522,6 +529,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<double>& a, bool akc, bool bkc, const Pr
         return launch_mfma<double, 128, 64, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F64_64x128:
         return launch_mfma<double, 64, 128, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
+    case F64_64x64:
+        return launch_mfma<double, 64, 64, 16, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F64_SMALL:
         return launch_small(a, akc, bkc, nb, s, 4);
     default:

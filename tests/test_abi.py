@@ -97,6 +97,7 @@ def test_noop_cases_need_no_device():
     (0, 0, 0, 0, 64, 80000, 2048, "mfma_f32_64x128x32_w2x2+splitk2"),  # 64x256 off whole rounds
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
+    (1, 0, 0, 0, 1024, 1024, 1024, "mfma_f64_64x64x16_w2x2"),  # fp64 mid-size: 64^2 tiles
 ])
 def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     sa = (k, m) if ta else (m, k)

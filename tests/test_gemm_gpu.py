@@ -536,6 +536,27 @@ def test_narrow_tiles(cuda, ta, tb):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp64_64x64_tile(cuda, ta, tb):
+    """The fp64 64x64 tile (four waves of 32x32, 16x16x4 fp64 MFMAs): ragged
+    edges with an odd K (a k-contiguous vector straddles K); a split tail
+    (1536^3, 4 parts).  Padded leading dimensions; the ldc padding of C
+    stays untouched.  Bar 1e-12."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k, want_name) in enumerate([(1500, 1300, 1023, "mfma_f64_64x64x16_w2x2"),
+                                              (1536, 1536, 1536, "mfma_f64_64x64x16_w2x2+splitk4")]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float64, 0, ta, tb, m, n, k, SEED + 110 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F64, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"fp64 64x64 case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == want_name, name
+        got = run_sbx(cuda, np.float64, 0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -1.25, C, ldc)
+        want = run_oracle(0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -1.25, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float64], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 def test_column_major_tall_skinny(cuda):
     """cfg4's shape (65536 x 64 x 4096) in column-major storage: C^T = B^T A^T
     makes it the wide row-major problem 64 x 65536 x 4096, which runs on the
