@@ -54,6 +54,7 @@ hipError_t launch_relu(T* x, int64_t n, hipStream_t stream);
     X(float, 64, 256, 32, 1, 8, 2, 2, 1) \
     X(float, 128, 32, 32, 4, 1, 2, 2, 1) \
     X(float, 32, 128, 32, 1, 4, 2, 2, 1) \
+    X(float, 64, 64, 32, 2, 2, 2, 2, 0) \
     X(double, 128, 128, 16, 2, 2, 1, 2, 0) \
     X(double, 128, 64, 16, 2, 2, 2, 2, 0) \
     X(double, 64, 128, 16, 2, 2, 2, 2, 0) \

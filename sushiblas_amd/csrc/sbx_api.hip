@@ -63,6 +63,7 @@ enum Cfg {
     F32_64x256,    // m <= 64 with a full round of 256-column tiles: 8 waves of 64x32 (16x16x4 MFMAs)
     F32_128x32,    // n <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
     F32_32x128,    // m <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
+    F32_64x64,     // fp32 mid-size: 4 waves of 32x32
     F64_128x128,   // fp64: 4 waves of 64x64, 2 waves/SIMD
     F64_128x64,
     F64_64x128,
@@ -86,6 +87,7 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
     {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},   {"mfma_f32_64x256x32_w1x8", 64, 256, 32, 1},
     {"mfma_f32_128x32x32_w4x1", 128, 32, 32, 2},   {"mfma_f32_32x128x32_w1x4", 32, 128, 32, 2},
+    {"mfma_f32_64x64x32_w2x2", 64, 64, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f64_64x64x16_w2x2", 64, 64, 16, 2},
     {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
@@ -166,6 +168,11 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         // one on most square-ish shapes, so it comes first
         out[c++] = wide;
         out[c++] = tall;
+        // fp32 mid-size: 64^2 tiles, after 64x128, which wins the shapes the
+        // model rates alike (2048^3: 121 against 127 us); 1024^3 NN 20
+        // against 27 us on the small-problem kernel, 1536^3 +splitk4 60
+        // against 73 us for 128^2 +splitk3
+        if (f32) out[c++] = F32_64x64;
     }
     out[c++] = f32 ? F32_SMALL : F64_SMALL;
     return c;
@@ -508,6 +515,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 128, 32, 32, 4, 1, 2, 2, 1>(a, akc, bkc, nb, s);
     case F32_32x128:
         return launch_mfma<float, 32, 128, 32, 1, 4, 2, 2, 1>(a, akc, bkc, nb, s);
+    case F32_64x64:
+        return launch_mfma<float, 64, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_SMALL:
         return launch_small(a, akc, bkc, nb, s, 4);
     case F32_SMALL8:
@@ -578,7 +587,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     Cfg cfg = GENERIC;
     SplitPlan sp{0, 1, 0};
     if (algo != SBX_ALGO_GENERIC) {
-        Cfg cands[5];
+        Cfg cands[6];
         const int64_t cus = cu_count();
         // no workspace for hipStreamPerThread: plan unsplit
         const size_t max_ws = fixed_ws ? fixed_bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
@@ -600,7 +609,13 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             // mirror only on whole rounds: off them the 64x128 tile with a
             // split tail was 2-4 % faster than it, split or not
             // (48x100000x1024, 64x70000x2048, 64x80000x2048).
-            const bool whole = tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1) % cus == 0;
+            const int64_t units = tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1);
+            const bool whole = units % cus == 0;
+            // The fp32 64^2 tile only up to two rounds (at two per CU): over
+            // more it ran 4-5 % behind the larger tiles, which the model
+            // rates alike (2048^3: 127 against 121 us for 64x128; 3000^3
+            // +splitk3: 415 against 394 us for 128^2 +splitk4).
+            if (cands[i] == F32_64x64 && units > 4 * cus) continue;
             if (cands[i] == F32_256x64 && c.sp.split == 1 && !whole) continue;
             if (cands[i] == F32_64x256 && !whole) continue;
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default

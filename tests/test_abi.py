@@ -109,11 +109,11 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
 
 
 @pytest.mark.parametrize("m,n,k,expect", [
-    (1024, 1024, 1024, "mfma_f32_32x32_ksplit4"),              # 1024 32^2 tiles: 4 per CU
+    (1024, 1024, 1024, "mfma_f32_64x64x32_w2x2"),              # 256 64^2 tiles: 20 against 27 us
     (512, 1024, 1024, "mfma_f32_32x32_ksplit4"),
     (2048, 2048, 2048, "mfma_f32_64x128x32_w2x2"),             # one full round of 512 slots
     (3000, 3000, 3000, "mfma_f32_128x128x16_w2x2+splitk4"),    # a full round + a 64-tile tail
-    (1536, 1536, 4096, "mfma_f32_128x128x16_w2x2+splitk7"),
+    (1536, 1536, 4096, "mfma_f32_64x64x32_w2x2+splitk4"),       # 142 against 158 us
     (4095, 3001, 2047, "mfma_f32_128x128x16_w2x2_o3"),         # 768 tiles: one round at 3 per CU
     (3584, 3584, 1536, "mfma_f32_128x128x16_w2x2_o3+splitk11"),
     (4096, 4096, 1024, "mfma_f32_256x128x16_w4x1"),       # 512 256x128 tiles: one round at 2 per CU
@@ -125,9 +125,9 @@ def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     (256, 256, 256, "mfma_f32_32x32_ksplit4"),                 # one launch: 64 tiles of 32^2
     (128, 1024, 512, "mfma_f32_32x32_ksplit8"),                # 128 tiles, K = 512: 8 waves
     (2000, 100, 500, "mfma_f32_32x32_ksplit4"),
-    (512, 512, 2048, "mfma_f32_32x32_ksplit8"),                # 256 32^2 tiles, K over 8 waves
-    (256, 256, 65536, "mfma_f32_64x128x32_w2x2+splitk32"),     # 8 tiles: a 32-way split fills the CUs
-    (325, 351, 12266, "mfma_f32_64x128x32_w2x2+splitk14"),
+    (512, 512, 2048, "mfma_f32_64x64x32_w2x2+splitk4"),         # 16 against 19 us
+    (256, 256, 65536, "mfma_f32_64x64x32_w2x2+splitk32"),      # 16 tiles: a 32-way split
+    (325, 351, 12266, "mfma_f32_64x64x32_w2x2+splitk14"),
 ])
 def test_model_based_selection(m, n, k, expect):
     """Tile shape and split from the cost model (whole rounds unsplit, the

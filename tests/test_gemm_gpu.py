@@ -537,6 +537,30 @@ def test_narrow_tiles(cuda, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp32_64x64_tile(cuda, ta, tb):
+    """The fp32 64x64 tile (four waves of 32x32 on 32x32x2 MFMAs): ragged
+    edges with K = 1023 (a k-contiguous vector straddles K) and with
+    misaligned bases; a split tail (1536 x 1536 x 1024, 4 parts).  Padded
+    leading dimensions; the ldc padding of C stays untouched."""
+    import sushiblas_amd as sbx
+    for i, (m, n, k, off, want_name) in enumerate([
+            (1000, 1100, 1023, (0, 0, 0), "mfma_f32_64x64x32_w2x2"),
+            (999, 1001, 1025, (1, 2, 3), "mfma_f32_64x64x32_w2x2"),
+            (1536, 1536, 1024, (0, 0, 0), "mfma_f32_64x64x32_w2x2+splitk4")]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 115 + i,
+                                             pad=(3, 1, 5))
+        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
+        print(f"fp32 64x64 case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
+        assert name == want_name, name
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.25, C, ldc,
+                      offsets=off)
+        want = run_oracle(0, ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.25, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_fp64_64x64_tile(cuda, ta, tb):
     """The fp64 64x64 tile (four waves of 32x32, 16x16x4 fp64 MFMAs): ragged
     edges with an odd K (a k-contiguous vector straddles K); a split tail
@@ -636,7 +660,7 @@ def test_split_k_is_deterministic(cuda, dtype):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_long_k_wide_splits(cuda, dtype):
     """Small outputs over a long K: the tail is cut into up to 32 k-ranges
-    (256 x 256 x 65536: 8 tiles, 32 parts each), and the reduction sums up
+    (256 x 256 x 65536: 16 tiles, 32 parts each), and the reduction sums up
     to 32 partials per element in part order.  Ragged edges, padded leading
     dimensions and a K tail on the second shape; whole results against the
     oracle, the ldc padding untouched, two runs bit-identical."""
@@ -665,11 +689,11 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 512), (1280, 1664, 2048)]
-    # 10 x 13 = 130 tiles of 128x128, all short of one round, each cut into
-    # >= 5 parts of 64 KiB: > 32 MiB of partials
-    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 1280, 1664, 2048, 2048, 1664, 1664)
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 5, name
+    shapes = [(512, 512, 512), (1920, 2816, 4096)]
+    # 15 x 22 = 330 tiles of 128x128, all short of one round, each cut into
+    # >= 3 parts of 64 KiB: > 32 MiB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 1920, 2816, 4096, 4096, 2816, 2816)
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 3, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)
@@ -728,7 +752,7 @@ def test_split_k_per_thread_streams(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(1024, 1024, 4096), (384, 320, 3000)]
+    shapes = [(1536, 1536, 1024), (384, 320, 3000)]
     data = []
     for i, (m, n, k) in enumerate(shapes):
         name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
@@ -782,7 +806,7 @@ def test_per_thread_stream_runs_unsplit(cuda):
     calling thread, match the oracle and allocate nothing."""
     import torch
     import sushiblas_amd as sbx
-    m, n, k = 1024, 1024, 4096
+    m, n, k = 1536, 1536, 1024
     assert "+splitk" in sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 81)
     want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
@@ -829,7 +853,7 @@ def test_split_k_when_the_workspace_cannot_be_allocated(cuda):
     import sushiblas_amd as sbx
     # the runtime torch loaded (loading another would start a second one)
     hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
-    m, n, k = 1024, 1024, 4096
+    m, n, k = 1536, 1536, 1024
     assert "+splitk" in sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 79)
     want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
@@ -892,7 +916,7 @@ def test_split_k_on_two_streams(cuda):
     streams do not corrupt each other."""
     import torch
     import sushiblas_amd as sbx
-    m, n, k = 1024, 1024, 4096
+    m, n, k = 1536, 1536, 1024
     assert "+splitk" in sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 71)
     want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)

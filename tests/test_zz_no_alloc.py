@@ -61,18 +61,18 @@ def test_noalloc_matches_gemm_ex_two_calls(cuda, dtype):
 
 
 def test_noalloc_bounds_the_split_to_the_scratch(cuda):
-    """A problem whose preferred split needs more than the scratch (130
-    tiles of 128x128 cut 5+ ways: > 32 MiB of partials) runs with a split
+    """A problem whose preferred split needs more than the scratch (330
+    tiles of 128x128 cut 3 ways: 62 MiB of partials) runs with a split
     that fits; the result stays within tolerance of the oracle and of
     sbx_gemm_ex.  A second, smaller call follows."""
     import torch
     import sushiblas_amd as sbx
     stream = torch.cuda.Stream()
-    m, n, k = 1280, 1664, 2048
+    m, n, k = 1920, 2816, 4096
     name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     parts = int(name.split("splitk")[1])
-    # 10 x 13 = 130 tiles, all short of one round
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and 130 * parts * 128 * 128 * 4 > SCRATCH, name
+    # 15 x 22 = 330 tiles, all short of one round
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and 330 * parts * 128 * 128 * 4 > SCRATCH, name
     for i, (mm, nn, kk) in enumerate([(m, n, k), (640, 640, 4096)]):
         ref, got, want, ldc = _run_both(cuda, np.float32, mm, nn, kk, 1.0, 0.5, SEED + 10 + i,
                                         stream)
@@ -85,7 +85,7 @@ def test_noalloc_bounds_the_split_to_the_scratch(cuda):
 def test_noalloc_allocates_nothing(cuda):
     """On a stream it has never seen, a split-K call of sbx_gemm_ex_noalloc
     takes no device memory (sbx_gemm_ex would allocate that stream's
-    workspace, at least 32 MiB, unless a pooled one is free)."""
+    workspace, at least 32 MiB)."""
     import torch
     import sushiblas_amd as sbx
     m, n, k = 1536, 1536, 1024
