@@ -100,7 +100,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Tile configurations worth modelling for a problem, the default first; cus
 // is the device's CU count (the round size of one-per-CU tiles).  *large is
-// set for the large-fp32 candidates, whose model adds an epilogue term.
+// set for the large-fp32 candidates, whose model adds an epilogue term.  At
+// most kMaxCands are written (the fp32 branch of mid-size shapes has six).
+constexpr int kMaxCands = 6;
 int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out, bool* large)
 {
     *large = false;
@@ -587,7 +589,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     Cfg cfg = GENERIC;
     SplitPlan sp{0, 1, 0};
     if (algo != SBX_ALGO_GENERIC) {
-        Cfg cands[6];
+        Cfg cands[kMaxCands];
         const int64_t cus = cu_count();
         // no workspace for hipStreamPerThread: plan unsplit
         const size_t max_ws = fixed_ws ? fixed_bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
