@@ -289,6 +289,10 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
 constexpr double kSmallRate = 0.21e12;
 constexpr double kSmallCuRate = 0.31e12;
 constexpr double kSmallF64Rate = 0.7;
+// fp64 past one tile per CU: the CU's throughput falls short of
+// kSmallF64Rate x kSmallCuRate (fp64 NN 576^3 took 19.5 us and 768^3 31.7,
+// 0.13-0.17 TFLOP/s per CU; the 64^2 tile 16.3 and 27.6)
+constexpr double kSmallF64CuRate = 0.52;
 // Its operand bytes at kSmallBw bound it too: a long reduction over a wide
 // operand streams (32 x 65536 x 4096: 283 us measured, 218 from the rates
 // alone -- 1.07 GB at 3.8 TB/s -- and 241 for the 64x256 tile).  The shapes
@@ -335,7 +339,8 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi 
         const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
         const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
         const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
-        const double thr = (double)cdiv(units, cus) * w / (kSmallCuRate * f);
+        const double thr = (double)cdiv(units, cus) * w /
+                           (kSmallCuRate * (c == F64_SMALL ? kSmallF64CuRate : 1.0));
         const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
         const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
                              (double)(p.batch > 1 ? p.batch : 1);
