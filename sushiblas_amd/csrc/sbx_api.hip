@@ -135,12 +135,16 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         // workgroups (65536 x 64 x 4096: 291-294 us against 296-300)
         if (f32 && cdiv(m, 256) >= cus) out[c++] = F32_256x64;
         out[c++] = tall;
+        // last, so that ties keep the tiles above: m <= 64 too (a batch of
+        // 64^3 problems: 128x64 spends half its MFMAs on padding)
+        if (f32) out[c++] = F32_64x64;
     } else if (m <= 64) {
         // the mirror of the tall case (column-major tall-skinny calls land
         // here): 64 x 65536 x 4096 270-272 against 280-284 us for 64x128
         if (f32 && m <= 32) out[c++] = F32_32x128;  // (32 x 65536 x 4096: 166 against 245 us)
         if (f32 && cdiv(n, 256) >= cus) out[c++] = F32_64x256;
         out[c++] = wide;
+        if (f32) out[c++] = F32_64x64;
     } else if (f32 && cdiv(m, 256) * cdiv(n, 256) >= cus * 3 / 4) {
         // Large fp32.  Two 256x128 workgroups per CU (64x128 per wave)
         // overlap each other's prologue and epilogue; they beat the 256^2
@@ -296,8 +300,14 @@ constexpr double kSmallF64CuRate = 0.52;
 // Its operand bytes at kSmallBw bound it too: a long reduction over a wide
 // operand streams (32 x 65536 x 4096: 283 us measured, 218 from the rates
 // alone -- 1.07 GB at 3.8 TB/s -- and 241 for the 64x256 tile).  The shapes
-// the rates were fitted on move too few bytes for this to bind.
+// the rates were fitted on move too few bytes for this to bind.  A batch
+// of small problems streams its problems' own contiguous slabs faster, at
+// kSmallBwBatch (1024 x 32 x 32 x 512 read 138 MB in 22.4 us, 6.2 TB/s,
+// where 4 TB/s sent it to a tile kernel taking 36.5; the bound still keeps
+// 512 x 64^3 on the 64^2 tile, 9.7 against 11.1 us fp32, 15.1 against
+// 21.2 fp64).
 constexpr double kSmallBw = 4e12;
+constexpr double kSmallBwBatch = 5e12;
 
 // Large fp32 shapes (epi set): a tile's epilogue moves its C tile, and the
 // CU's other workgroups hide only part of that time.  The model adds, per
@@ -344,8 +354,9 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi 
         const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
         const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
                              (double)(p.batch > 1 ? p.batch : 1);
+        const double stream = bytes / (p.batch > 1 ? kSmallBwBatch : kSmallBw);
         const double compute = (lat > thr ? lat : thr) * lay;
-        const double t = 1.5e-6 + (compute > bytes / kSmallBw ? compute : bytes / kSmallBw);
+        const double t = 1.5e-6 + (compute > stream ? compute : stream);
         return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
     }
     const CfgInfo& ci = kCfg[c];
