@@ -136,8 +136,12 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         if (f32 && cdiv(m, 256) >= cus) out[c++] = F32_256x64;
         out[c++] = tall;
         // last, so that ties keep the tiles above: m <= 64 too (a batch of
-        // 64^3 problems: 128x64 spends half its MFMAs on padding)
-        if (f32) out[c++] = F32_64x64;
+        // 64^3 problems: 128x64 spends half its MFMAs on padding).  fp64
+        // only where m <= 64 as well: 512 x 64^3 11.4 against 14.8 us,
+        // 64 x 64 x 8192 +splitk31 16.0 against 23.9 us; with a long m the
+        // small-problem kernel or 128x64 stays ahead (40000 x 32 x 2048:
+        // 152 against 179 us, 24 x 100000 x 1024: 183 against 211 us)
+        if (f32 || m <= 64) out[c++] = f32 ? F32_64x64 : F64_64x64;
     } else if (m <= 64) {
         // the mirror of the tall case (column-major tall-skinny calls land
         // here): 64 x 65536 x 4096 270-272 against 280-284 us for 64x128

@@ -98,6 +98,9 @@ def test_noop_cases_need_no_device():
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
     (1, 0, 0, 0, 1024, 1024, 1024, "mfma_f64_64x64x16_w2x2"),  # fp64 mid-size: 64^2 tiles
+    (1, 0, 0, 0, 64, 64, 8192, "mfma_f64_64x64x16_w2x2+splitk31"),  # m, n <= 64: 16 against 24 us
+    (1, 0, 0, 0, 40000, 32, 2048, "mfma_f64_32x32_ksplit4"),  # long m: not the 64^2 tile
+    (1, 0, 0, 0, 24, 100000, 1024, "mfma_f64_32x32_ksplit4"),
 ])
 def test_kernel_selection(dtype, layout, ta, tb, m, n, k, expect):
     sa = (k, m) if ta else (m, k)

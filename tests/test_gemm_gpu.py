@@ -564,11 +564,14 @@ def test_fp32_64x64_tile(cuda, ta, tb):
 def test_fp64_64x64_tile(cuda, ta, tb):
     """The fp64 64x64 tile (four waves of 32x32, 16x16x4 fp64 MFMAs): ragged
     edges with an odd K (a k-contiguous vector straddles K); a split tail
-    (1536^3, 4 parts).  Padded leading dimensions; the ldc padding of C
-    stays untouched.  Bar 1e-12."""
+    (1536^3, 4 parts); one tile cut 31 ways along a long K, whole and ragged
+    (m, n <= 64).  Padded leading dimensions; the ldc padding of C stays
+    untouched.  Bar 1e-12."""
     import sushiblas_amd as sbx
     for i, (m, n, k, want_name) in enumerate([(1500, 1300, 1023, "mfma_f64_64x64x16_w2x2"),
-                                              (1536, 1536, 1536, "mfma_f64_64x64x16_w2x2+splitk4")]):
+                                              (1536, 1536, 1536, "mfma_f64_64x64x16_w2x2+splitk4"),
+                                              (64, 64, 8192, "mfma_f64_64x64x16_w2x2+splitk31"),
+                                              (40, 17, 4099, "mfma_f64_64x64x16_w2x2+splitk31")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float64, 0, ta, tb, m, n, k, SEED + 110 + i,
                                              pad=(3, 1, 5))
         name = sbx.gemm_select(sbx.F64, 0, ta, tb, m, n, k, lda, ldb, ldc)
@@ -579,6 +582,36 @@ def test_fp64_64x64_tile(cuda, ta, tb):
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float64], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
         np.testing.assert_array_equal(got[outside], C[outside])
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 64), (40, 17, 70)])
+def test_fp64_batch_of_tiny_problems(cuda, m, n, k):
+    """A strided batch of 384 fp64 problems with m, n <= 64, where the model
+    offers the 64x64 tile beside the small-problem kernel (one tile per
+    problem, the batch entry on the grid's z axis), against the oracle
+    entry by entry.  Bar 1e-12."""
+    import torch
+    import sushiblas_amd as sbx
+    batch = 384
+    str_a, str_b, str_c = m * k + 2, k * n + 1, m * n + 3
+    A = oracle.fill_uniform(batch * str_a, np.float64, SEED + 120, 0)
+    B = oracle.fill_uniform(batch * str_b, np.float64, SEED + 120, 1)
+    C = oracle.fill_uniform(batch * str_c, np.float64, SEED + 120, 2)
+    print(f"fp64 tiny batch {batch} x {m}x{n}x{k}", flush=True)
+    dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
+    sbx.gemm_ex(sbx.F64, 0, 0, 0, m, n, k, -0.5, dA, k, str_a, dB, n, str_b, 1.25, dC, n, str_c,
+                batch)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    want = C.copy()
+    oracle.gemm_strided_batched(0, 0, 0, m, n, k, -0.5, A, k, str_a, B, n, str_b, 1.25, want, n,
+                                str_c, batch, 1)
+    for b in range(batch):
+        g = got[b * str_c:b * str_c + m * n].reshape(m, n)
+        w = want[b * str_c:b * str_c + m * n].reshape(m, n)
+        assert oracle.rel_fro_err(g, w) <= TOL[np.float64], b
+        np.testing.assert_array_equal(got[b * str_c + m * n:(b + 1) * str_c],
+                                      C[b * str_c + m * n:(b + 1) * str_c])
 
 
 def test_column_major_tall_skinny(cuda):
