@@ -206,6 +206,14 @@ int sbx_dsyrk_strided_batched(void* stream, int layout, int upper, int trans, in
 int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
                     int64_t k, int64_t lda, int64_t ldb, int64_t ldc, char* name, size_t cap);
 
+/* The same for a strided batch of `batch` packed entries (stride = the stored
+ * extent of each operand): a batch whose grid fills less than one round of
+ * the device cuts K too, so its pick can differ from a single problem's.
+ * No counterpart in the reference (introspection, as above). */
+int sbx_gemm_select_batched(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                            int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                            char* name, size_t cap);
+
 /* The same for sbx_{s,d}syrk[_strided_batched] (single problem): the kernel
  * and split that would compute the triangle. */
 int sbx_syrk_select(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,

@@ -96,6 +96,9 @@ def lib() -> ctypes.CDLL:
     L.sbx_gemm_select.restype = i32
     L.sbx_gemm_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64,
                                   ctypes.c_char_p, ctypes.c_size_t]
+    L.sbx_gemm_select_batched.restype = i32
+    L.sbx_gemm_select_batched.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, i64,
+                                          ctypes.c_char_p, ctypes.c_size_t]
     L.sbx_syrk_select.restype = i32
     L.sbx_syrk_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, ctypes.c_char_p,
                                   ctypes.c_size_t]
@@ -216,10 +219,15 @@ def syrk(dtype, layout, upper, trans, n, k, alpha, A, lda, str_a, beta, C, ldc, 
              str_a, beta, _ptr(C), ldc, str_c, batch), "sbx_syrk")
 
 
-def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc) -> str:
+def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc, batch=1) -> str:
     buf = ctypes.create_string_buffer(128)
-    _check(lib().sbx_gemm_select(dtype, layout, int(transA), int(transB), m, n, k, lda, ldb,
-                                 ldc, buf, 128), "sbx_gemm_select")
+    if batch == 1:
+        _check(lib().sbx_gemm_select(dtype, layout, int(transA), int(transB), m, n, k, lda, ldb,
+                                     ldc, buf, 128), "sbx_gemm_select")
+    else:
+        _check(lib().sbx_gemm_select_batched(dtype, layout, int(transA), int(transB), m, n, k,
+                                             lda, ldb, ldc, batch, buf, 128),
+               "sbx_gemm_select_batched")
     return buf.value.decode()
 
 

@@ -846,7 +846,9 @@ gemm_mfma_kernel(GemmArgs<T> p)
     // stay (local column c of local row m is global column n0 + c, row m0 + m)
     int lo_off = -(1 << 30), hi_off = 1 << 30;
     if (is_split) {
-        dst = (GT*)(p.ws + ((int64_t)(id - p.num_full) * p.split + part) * (BM * BN));
+        // batch entry z's partials follow those of entries 0 .. z-1
+        const int64_t slot = (int64_t)blockIdx.z * (p.tiles - p.num_full) + (id - p.num_full);
+        dst = (GT*)(p.ws + (slot * p.split + part) * (BM * BN));
         ldd = BN;
         row_lim = BM;
         col_lim = BN;
@@ -1000,7 +1002,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs<T> p)
     if (p.uplo == 1) hi = min(hi, m + 1);       // column <= row
     else if (p.uplo == 2) lo = max(lo, m);      // column >= row
     if (lo >= hi) return;
-    const GV* part0 = (const GV*)(p.ws + (int64_t)slot * p.split * (BM * BN) + e);
+    const int64_t zslot = (int64_t)blockIdx.z * (p.tiles - p.num_full) + slot;
+    const GV* part0 = (const GV*)(p.ws + zslot * p.split * (BM * BN) + e);
     constexpr int PV = (BM * BN) / RV;  // vectors per partial
     vec_t sum = part0[0];
     for (int q0 = 1; q0 < p.split; q0 += 16) {

@@ -308,7 +308,7 @@ constexpr double kSmallF64CuRate = 0.52;
 // of small problems streams its problems' own contiguous slabs faster, at
 // kSmallBwBatch (1024 x 32 x 32 x 512 read 138 MB in 22.4 us, 6.2 TB/s,
 // where 4 TB/s sent it to a tile kernel taking 36.5; the bound still keeps
-// 512 x 64^3 on the 64^2 tile, 9.7 against 11.1 us fp32, 15.1 against
+// 512 x 64^3 on the 64^2 tile, 9.7 against 11.1 us fp32, 11.4 against
 // 21.2 fp64).
 constexpr double kSmallBw = 4e12;
 constexpr double kSmallBwBatch = 5e12;
@@ -385,16 +385,23 @@ Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi 
     const int64_t units = tiles * (p.batch > 1 ? p.batch : 1);
     Choice best{c, SplitPlan{(int)tiles, 1, 0}, rounds_time(units, w, P, cus, e1) + F};
     const int64_t nk = cdiv(p.k, ci.bk);
-    if (p.batch > 1 || nk < 4) return best;
-    const int64_t rem = tiles >= P * cus ? tiles % (P * cus) : tiles;
+    if (nk < 4) return best;
+    // A batch splits every tile of every entry, and only where its grid
+    // fills less than one round of the chip (128 x 128^2 x 1024 on 128^2
+    // tiles: 128 workgroups for 512 slots).  Entry z's partials follow
+    // entry z-1's, so the workspace holds one launch's entries.
+    const int64_t nb = p.batch > 1 ? p.batch : 1;
+    const int64_t zmax = nb < kMaxGridZ ? nb : kMaxGridZ;
+    if (nb > 1 && units >= P * cus) return best;
+    const int64_t rem = nb > 1 ? tiles : tiles >= P * cus ? tiles % (P * cus) : tiles;
     if (rem == 0) return best;
     const int64_t full = tiles - rem;
     const int64_t smax = nk / 2 < kMaxSplit ? nk / 2 : kMaxSplit;
     for (int64_t sp = 2; sp <= smax; ++sp) {
-        if ((size_t)(rem * sp) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
-        const double t = rounds_time(full, w, P, cus, e1) +
-                         rounds_time(rem * sp, wk / (double)sp + o_part + kPartSec, P, cus, e1) + F + G +
-                         (double)(rem * sp) * ci.bm * ci.bn * elem / W;
+        if ((size_t)(rem * sp * zmax) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
+        const double t = rounds_time(full * nb, w, P, cus, e1) +
+                         rounds_time(rem * sp * nb, wk / (double)sp + o_part + kPartSec, P, cus, e1) +
+                         F + G + (double)(rem * sp * nb) * ci.bm * ci.bn * elem / W;
         if (t < best.seconds * 0.98)
             best = Choice{c, SplitPlan{(int)full, (int)sp, (int)rem}, t};
     }
@@ -664,7 +671,9 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
     void* ws = nullptr;
     WorkspaceLease lease;  // held until both split kernels are enqueued
-    const size_t ws_bytes = (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T);
+    // one launch's batch entries (at most kMaxGridZ) each hold their partials
+    const int64_t zmax = p.batch < 1 ? 1 : p.batch < kMaxGridZ ? p.batch : kMaxGridZ;
+    const size_t ws_bytes = (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T) * (size_t)zmax;
     if (sp.split > 1 && fixed_ws) {
         // the planner keeps every split's partials within fixed_bytes; a plan
         // that did not fit would be refused here, never written past the end
@@ -1128,7 +1137,21 @@ int sbx_dgemm_strided_batched(void* stream, int layout, int transA, int transB, 
 int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
                     int64_t k, int64_t lda, int64_t ldb, int64_t ldc, char* name, size_t cap)
 {
+    return sbx_gemm_select_batched(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc, 1, name,
+                                   cap);
+}
+
+int sbx_gemm_select_batched(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                            int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                            char* name, size_t cap)
+{
     if (!name || cap == 0) return SBX_INVALID_ARGUMENT;
+    if (batch < 1) return SBX_INVALID_ARGUMENT;
+    // packed entries: each stride is its operand's stored extent
+    const int64_t rows_a = (layout == 0) == !transA ? m : k;
+    const int64_t rows_b = (layout == 0) == !transB ? k : n;
+    const int64_t rows_c = layout == 0 ? m : n;
+    const int64_t str_a = rows_a * lda, str_b = rows_b * ldb, str_c = rows_c * ldc;
     static const float one_f = 1.0f;
     static const double one_d = 1.0;
     const void* one = dtype == SBX_F64 ? (const void*)&one_d : (const void*)&one_f;
@@ -1136,9 +1159,9 @@ int sbx_gemm_select(int dtype, int layout, int transA, int transB, int64_t m, in
     const void* fake = (const void*)(uintptr_t)0x1000;
     sbx::Cfg cfg = sbx::GENERIC;
     sbx::SplitPlan sp{0, 1, 0};
-    int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda, 0,
-                            fake, ldb, 0, one, (void*)fake, ldc, 0, 1, SBX_ALGO_AUTO,
-                            SBX_EPILOGUE_NONE, &cfg, &sp);
+    int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda,
+                            str_a, fake, ldb, str_b, one, (void*)fake, ldc, str_c, batch,
+                            SBX_ALGO_AUTO, SBX_EPILOGUE_NONE, &cfg, &sp);
     if (st != SBX_OK) return st;
     if (sp.split > 1)
         snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);

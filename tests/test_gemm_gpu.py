@@ -614,6 +614,48 @@ def test_fp64_batch_of_tiny_problems(cuda, m, n, k):
                                       C[b * str_c + m * n:(b + 1) * str_c])
 
 
+@pytest.mark.parametrize("dtype,layout,ta,tb,batch,m,n,k,want", [
+    (np.float32, 0, 0, 0, 3, 300, 200, 5000, "mfma_f32_64x128x32_w2x2+splitk17"),
+    (np.float64, 0, 0, 0, 3, 300, 200, 5000, "mfma_f64_64x64x16_w2x2+splitk8"),
+    (np.float32, 1, 1, 0, 5, 130, 257, 3001, "mfma_f32_64x64x32_w2x2+splitk3"),
+    (np.float64, 0, 1, 1, 2, 77, 500, 6000, "mfma_f64_64x64x16_w2x2+splitk8"),
+])
+def test_split_k_strided_batch(cuda, dtype, layout, ta, tb, batch, m, n, k, want):
+    """A batch whose grid fills less than one round cuts K: every entry's
+    tiles are split, entry z's partials after entry z-1's in the workspace,
+    and the reduction finishes each entry's C (alpha, beta) in part order.
+    Each entry against the oracle, and the padding between entries of C
+    untouched.  Bars 1e-5 / 1e-12."""
+    import torch
+    import sushiblas_amd as sbx
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    sa = (k, m) if ta else (m, k)
+    sb = (n, k) if tb else (k, n)
+    lda = sa[1] if layout == 0 else sa[0]
+    ldb = sb[1] if layout == 0 else sb[0]
+    ldc = n if layout == 0 else m
+    assert sbx.gemm_select(code, layout, ta, tb, m, n, k, lda, ldb, ldc, batch=batch) == want
+    str_a, str_b, str_c = sa[0] * sa[1], sb[0] * sb[1], m * n + 4
+    A = oracle.fill_uniform(batch * str_a, dtype, SEED + 130, 0)
+    B = oracle.fill_uniform(batch * str_b, dtype, SEED + 130, 1)
+    C = oracle.fill_uniform(batch * str_c, dtype, SEED + 130, 2)
+    print(f"split batch {batch} x {m}x{n}x{k} layout={layout} t{ta}{tb} -> {want}", flush=True)
+    dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
+    sbx.gemm_ex(code, layout, ta, tb, m, n, k, 0.75, dA, lda, str_a, dB, ldb, str_b, -0.5, dC,
+                ldc, str_c, batch)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    want_c = C.copy()
+    oracle.gemm_strided_batched(layout, ta, tb, m, n, k, 0.75, A, lda, str_a, B, ldb, str_b, -0.5,
+                                want_c, ldc, str_c, batch, 1)
+    for b in range(batch):
+        g = c_window(layout, got[b * str_c:b * str_c + m * n], m, n, ldc)
+        w = c_window(layout, want_c[b * str_c:b * str_c + m * n], m, n, ldc)
+        assert oracle.rel_fro_err(g, w) <= TOL[dtype], b
+        np.testing.assert_array_equal(got[b * str_c + m * n:(b + 1) * str_c],
+                                      C[b * str_c + m * n:(b + 1) * str_c])
+
+
 def test_column_major_tall_skinny(cuda):
     """cfg4's shape (65536 x 64 x 4096) in column-major storage: C^T = B^T A^T
     makes it the wide row-major problem 64 x 65536 x 4096, which runs on the

@@ -281,6 +281,10 @@ def test_syrk_padded_unaligned_batched(cuda, dtype):
         got, want, C0 = run_syrk(cuda, dtype, 1, upper, 1, 97, 200, -1.0, 1.0, SEED + 21,
                                  batch=4, gaps=(7, 9))
         _check_syrk(got, want, C0, dtype)
+        # a batch of few triangle tiles and a long K: every entry's tiles split
+        got, want, C0 = run_syrk(cuda, dtype, 0, upper, 0, 200, 3000, 0.5, -1.0, SEED + 22,
+                                 batch=3, gaps=(5, 3))
+        _check_syrk(got, want, C0, dtype)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
