@@ -110,3 +110,40 @@ def test_noalloc_allocates_nothing(cuda):
     torch.cuda.synchronize()
     free1 = torch.cuda.mem_get_info()[0]
     assert free0 - free1 < (1 << 20), (free0, free1)
+
+
+def test_noalloc_split_batch_two_calls(cuda):
+    """Strided batches that cut K (their grids fill less than one round):
+    every entry's partials sit in the scratch after the previous entry's.
+    Two calls in a row on one stream, the second with a smaller batch and a
+    different tile, both fit the scratch, so the bits match sbx_gemm_ex's;
+    each entry within tolerance of the oracle."""
+    import torch
+    import oracle
+    import sushiblas_amd as sbx
+    stream = torch.cuda.Stream()
+    for i, (batch, m, n, k) in enumerate([(8, 128, 128, 4096), (3, 300, 200, 5000)]):
+        name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n, batch=batch)
+        print(f"noalloc split batch {batch} x {m}x{n}x{k} -> {name}", flush=True)
+        assert "+splitk" in name, name
+        str_a, str_b, str_c = m * k, k * n, m * n
+        A = oracle.fill_uniform(batch * str_a, np.float32, SEED + 20 + i, 0)
+        B = oracle.fill_uniform(batch * str_b, np.float32, SEED + 20 + i, 1)
+        C = oracle.fill_uniform(batch * str_c, np.float32, SEED + 20 + i, 2)
+        dA, dB = torch.from_numpy(A).to(cuda), torch.from_numpy(B).to(cuda)
+        c_ref, c_na = torch.from_numpy(C).to(cuda), torch.from_numpy(C).to(cuda)
+        torch.cuda.synchronize()
+        sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 0.5, dA, k, str_a, dB, n, str_b, 1.5, c_ref, n,
+                    str_c, batch, stream=stream)
+        sbx.gemm_ex_noalloc(sbx.F32, 0, 0, 0, m, n, k, 0.5, dA, k, str_a, dB, n, str_b, 1.5, c_na,
+                            n, str_c, batch, stream=stream)
+        torch.cuda.synchronize()
+        ref, got = c_ref.cpu().numpy(), c_na.cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint8), ref.view(np.uint8))
+        want = C.copy()
+        oracle.gemm_strided_batched(0, 0, 0, m, n, k, 0.5, A, k, str_a, B, n, str_b, 1.5, want, n,
+                                    str_c, batch, 1)
+        for b in range(batch):
+            w = want[b * str_c:(b + 1) * str_c].reshape(m, n)
+            g = got[b * str_c:(b + 1) * str_c].reshape(m, n)
+            assert oracle.rel_fro_err(g, w) <= TOL[np.float32], b
