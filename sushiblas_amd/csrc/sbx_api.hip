@@ -645,6 +645,17 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             // rates alike (2048^3: 127 against 121 us for 64x128; 3000^3
             // +splitk3: 415 against 394 us for 128^2 +splitk4).
             if (cands[i] == F32_64x64 && units > 4 * cus) continue;
+            // Nor for a batch whose entries the 64x128 tile covers exactly:
+            // its larger wave tile wins although the model rates the 64^2
+            // grid's finer rounds ahead (128 x 128^2 x 1024: 35.4 against
+            // 42.1 us, 64 x 128^2 x 2048: 43.9 against 55.0); where both
+            // pad (16 x 200^2 x 2000: 36.5 against 40.2 us) or only 64x128
+            // does (32 x 192^2 x 1536 +splitk3: 46.1 against 59.1), 64^2
+            // stays ahead, as it does split (8 x 128^2 x 4096 +splitk8:
+            // 16.2 us).
+            if (cands[i] == F32_64x64 && p.batch > 1 && c.sp.split == 1 && p.m % 64 == 0 &&
+                p.n % 128 == 0)
+                continue;
             if (cands[i] == F32_256x64 && c.sp.split == 1 && !whole) continue;
             if (cands[i] == F32_64x256 && !whole) continue;
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
