@@ -656,6 +656,16 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             if (cands[i] == F32_64x64 && p.batch > 1 && c.sp.split == 1 && p.m % 64 == 0 &&
                 p.n % 128 == 0)
                 continue;
+            // fp64 likewise, where the 64x128 grid fills one to two workgroups
+            // per CU unsplit (128 x 128^2 x 1024: 70.9 against 106.0 us, 64 x
+            // 256^3: 38.5 against 41.5); with fewer it splits and with more
+            // its part round trails, and 64^2 led (16 x 256^2 x 2048: 67.8
+            // against 73.0 us, 32 x 384^3: 68.8 against 74.6).
+            if (cands[i] == F64_64x64 && p.batch > 1 && c.sp.split == 1 && p.m % 64 == 0 &&
+                p.n % 128 == 0) {
+                const int64_t wu = tile_count(p, F64_64x128) * p.batch;
+                if (wu >= cus && wu <= 2 * cus) continue;
+            }
             if (cands[i] == F32_256x64 && c.sp.split == 1 && !whole) continue;
             if (cands[i] == F32_64x256 && !whole) continue;
             if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default

@@ -147,6 +147,10 @@ def test_model_based_selection(m, n, k, expect):
     (0, 64, 128, 128, 2048, "mfma_f32_64x128x32_w2x2+splitk4"),
     (1, 3, 300, 200, 5000, "mfma_f64_64x64x16_w2x2+splitk8"),
     (1, 512, 64, 64, 64, "mfma_f64_64x64x16_w2x2"),              # m, n <= 64: 64^2 tile
+    (1, 128, 128, 128, 1024, "mfma_f64_64x128x16_w2x2"),         # 64x128: one per CU
+    (1, 64, 256, 256, 256, "mfma_f64_64x128x16_w2x2"),           # two per CU
+    (1, 16, 256, 256, 2048, "mfma_f64_64x64x16_w2x2"),           # 64x128 would split
+    (1, 32, 384, 384, 384, "mfma_f64_64x64x16_w2x2"),            # 64x128 part round
     (0, 1024, 32, 32, 512, "mfma_f32_32x32_ksplit4"),            # streams its slabs
 ])
 def test_batched_selection(dtype, batch, m, n, k, expect):
