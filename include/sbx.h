@@ -121,10 +121,15 @@ int sbx_gemm_ex(void* stream, int dtype, int layout, int transA, int transB, int
  * splits whose partials fit in it (a problem whose preferred split would not
  * fit runs with fewer k-parts or unsplit, so results may differ from
  * sbx_gemm_ex by rounding only; none is refused for its size).  It calls no
- * hipMalloc/hipFree.  Every call on one GPU shares that GPU's array: calls
- * whose split kernels overlap on one GPU (different streams, not ordered by
- * the caller) race on it; calls ordered on one stream do not.  Every partial
- * is written before it is read, so nothing in the array needs clearing. */
+ * hipMalloc/hipFree.  Every call on one GPU shares that GPU's array.  A call
+ * that splits holds a per-GPU host lock while it enqueues its two kernels
+ * (the partial pass and the reduction), so concurrent host threads are
+ * serialised at enqueue: on one stream, one call's kernels never interleave
+ * with another's, whatever thread issued them.  Calls on different streams
+ * of one GPU are not ordered by that lock: when their kernels run at the
+ * same time they race on the array, and the caller must order them (one
+ * stream, or events).  Every partial is written before it is read, so
+ * nothing in the array needs clearing. */
 int sbx_gemm_ex_noalloc(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
                         int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
                         int64_t str_a, const void* B, int64_t ldb, int64_t str_b,

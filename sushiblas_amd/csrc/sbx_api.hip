@@ -605,11 +605,21 @@ int stream_operand(const Problem& p, int tiles_m, int tiles_n)
     return 0;
 }
 
-// fixed_ws / fixed_bytes: caller-provided split workspace (the
-// allocation-free entry point's scratch); null: the stream's cached one.
+// A caller-provided split workspace: the allocation-free entry point's
+// per-device scratch.  `launch_mu` plays the part of Workspace::launch_mu:
+// it is held from handing out the scratch until the split kernels are
+// enqueued, so another host thread's call (on the same stream or not) never
+// lands between one call's partial writes and their reduction.
+struct FixedScratch {
+    void* ptr;
+    size_t bytes;
+    std::mutex* launch_mu;
+};
+
+// fixed: the caller's split workspace; null: the stream's cached one.
 template <typename T>
 int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen,
-        SplitPlan* chosen_split, void* fixed_ws = nullptr, size_t fixed_bytes = 0)
+        SplitPlan* chosen_split, const FixedScratch* fixed = nullptr)
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
@@ -619,7 +629,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         Cfg cands[kMaxCands];
         const int64_t cus = cu_count();
         // no workspace for hipStreamPerThread: plan unsplit
-        const size_t max_ws = fixed_ws ? fixed_bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
+        const size_t max_ws = fixed ? fixed->bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
         bool large = false;
         const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
         bool any = false;
@@ -692,14 +702,16 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
     if (stream == (hipStream_t)-1) return SBX_OK;  // selection only
     void* ws = nullptr;
     WorkspaceLease lease;  // held until both split kernels are enqueued
+    std::unique_lock<std::mutex> scratch_lock;  // the same, for the fixed scratch
     // one launch's batch entries (at most kMaxGridZ) each hold their partials
     const int64_t zmax = p.batch < 1 ? 1 : p.batch < kMaxGridZ ? p.batch : kMaxGridZ;
     const size_t ws_bytes = (size_t)sp.rem * sp.split * info.bm * info.bn * sizeof(T) * (size_t)zmax;
-    if (sp.split > 1 && fixed_ws) {
-        // the planner keeps every split's partials within fixed_bytes; a plan
+    if (sp.split > 1 && fixed) {
+        // the planner keeps every split's partials within fixed->bytes; a plan
         // that did not fit would be refused here, never written past the end
-        if (ws_bytes > fixed_bytes) return SBX_UNSUPPORTED;
-        ws = fixed_ws;
+        if (ws_bytes > fixed->bytes) return SBX_UNSUPPORTED;
+        scratch_lock = std::unique_lock<std::mutex>(*fixed->launch_mu);
+        ws = fixed->ptr;
     } else if (sp.split > 1) {
         if (lease.acquire(stream, ws_bytes))
             ws = lease.ptr;
@@ -754,8 +766,7 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
               int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
               int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
               void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, int epilogue,
-              Cfg* chosen, SplitPlan* chosen_split, void* fixed_ws = nullptr,
-              size_t fixed_bytes = 0)
+              Cfg* chosen, SplitPlan* chosen_split, const FixedScratch* fixed = nullptr)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
@@ -803,9 +814,9 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen,
-                          chosen_split, fixed_ws, fixed_bytes);
+                          chosen_split, fixed);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
-                       chosen_split, fixed_ws, fixed_bytes);
+                       chosen_split, fixed);
 }
 
 // Grouped GEMM: `count` problems of one shape and one set of scalars whose
@@ -991,19 +1002,23 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[64] = {nullptr};
+// per device: held while one call enqueues the kernels that use the scratch
+std::mutex g_scratch_launch_mu[64];
 
-// The current device's address of `scratch`; null if the lookup fails.
-void* device_scratch()
+// The current device's scratch (address of `scratch`, its size and launch
+// lock); false if the lookup fails.
+bool device_scratch(FixedScratch* out)
 {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
     std::lock_guard<std::mutex> g(g_scratch_mutex);
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return false;
         g_scratch_ptr[dev] = p;
     }
-    return g_scratch_ptr[dev];
+    *out = FixedScratch{g_scratch_ptr[dev], kScratchBytes, &g_scratch_launch_mu[dev]};
+    return true;
 }
 
 }  // namespace
@@ -1029,11 +1044,11 @@ int sbx_gemm_ex_noalloc(void* stream, int dtype, int layout, int transA, int tra
                         int algo)
 {
     if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
-    void* ws = sbx::device_scratch();
-    if (!ws) return SBX_HIP_ERROR;
+    sbx::FixedScratch ws;
+    if (!sbx::device_scratch(&ws)) return SBX_HIP_ERROR;
     return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
                           B, ldb, str_b, beta, C, ldc, str_c, batch, algo, SBX_EPILOGUE_NONE,
-                          nullptr, nullptr, ws, sbx::kScratchBytes);
+                          nullptr, nullptr, &ws);
 }
 
 int sbx_gemm_fused(void* stream, int dtype, int layout, int transA, int transB, int64_t m,

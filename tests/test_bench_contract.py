@@ -38,3 +38,23 @@ def test_traffic_is_read_from_the_bytes_column():
         assert abs(got - (fetch * ff + write * fw) * 1024) <= 1e-3 * got + 4096, workload
         assert abs(got / algorithmic - float(cells[6])) < 0.006, workload
     assert bench.read_traffic("no_such_workload") is None
+
+
+def test_cpu_leg_reports_the_mkl_stand_in_with_the_port_nested():
+    """cpu_baseline.value is the reference CPU path's stand-in (MKL through
+    torch's CPU addmm); the oracle port is nested under `port`; parity covers
+    the whole matrix.  A small problem, so it runs in well under a second."""
+    import numpy as np
+    import bench
+    import oracle
+    m, n, k = 96, 80, 72
+    A = oracle.fill_uniform(m * k, np.float32, 7, 0)
+    B = oracle.fill_uniform(k * n, np.float32, 7, 1)
+    C = oracle.fill_uniform(m * n, np.float32, 7, 2)
+    got = C.copy()
+    oracle.gemm(0, 0, 0, m, n, k, 1.5, A, k, B, n, 0.5, got, n, 1)
+    base, parity = bench.cpu_leg("f32", 0, 0, m, n, k, 1.5, 0.5, A, k, B, n, C, n, got, 0.01)
+    assert base["kind"] == "reference" and base["value"] > 0 and "MKL" in base["stand_in"]
+    assert base["normwise_vs_gpu"] <= 1e-5
+    assert base["port"]["kind"] == "port" and base["port"]["value"] > 0
+    assert parity["ok"] and parity["rows"] == m

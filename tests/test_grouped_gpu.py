@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 SEED = 20261209
 
 
-def _grouped(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, count, epilogue=0, misalign=False):
+def _grouped(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, count, epilogue=0, misalign=False,
+             pad=(0, 0, 0)):
     import torch
     import sushiblas_amd as sbx
     L = sbx.lib()
@@ -32,7 +33,7 @@ def _grouped(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, count, epilogue=
     off = 1 if misalign else 0
     problems, bufs, ptrs = [], [], []
     for i in range(count):
-        A, lda, B, ldb, C, ldc = make_inputs(dtype, layout, ta, tb, m, n, k, SEED + i)
+        A, lda, B, ldb, C, ldc = make_inputs(dtype, layout, ta, tb, m, n, k, SEED + i, pad=pad)
         # each operand in its own allocation, with guard elements before and after
         dev = []
         for x in (A, B, C):
@@ -66,8 +67,16 @@ def _grouped(cuda, dtype, layout, ta, tb, m, n, k, alpha, beta, count, epilogue=
             assert oracle.rel_fro_err(gw, ww) <= TOL[dtype]
         else:
             assert np.array_equal(gw, ww)
-        # guards around C untouched
+        # guards around C untouched, and C's elements outside the m x n window
+        # (the ld padding) keep their input bits
         assert np.all(got_full[:off] == -3.0) and np.all(got_full[off + C.size:] == -3.0)
+        outside = np.ones(C.size, bool)
+        idx = np.arange(C.size)
+        if layout == 0:
+            outside[(idx // ldc < m) & (idx % ldc < n)] = False
+        else:
+            outside[(idx // ldc < n) & (idx % ldc < m)] = False
+        assert np.array_equal(got[outside].view(np.uint8), C[outside].view(np.uint8))
         # A and B untouched too
         for x, d in ((A, dev[0]), (B, dev[1])):
             assert np.array_equal(d.cpu().numpy()[off:off + x.size], x)
@@ -86,3 +95,25 @@ def test_grouped_shapes_epilogue_quick_and_misaligned(cuda):
     _grouped(cuda, np.float32, 0, 1, 0, 300, 257, 129, 0.75, 0.25, 3, misalign=True)
     _grouped(cuda, np.float64, 1, 0, 1, 65, 33, 17, 0.0, 2.0, 4)                  # alpha == 0
     _grouped(cuda, np.float32, 0, 0, 0, 1000, 64, 512, 1.0, 0.0, 2)              # tall tiles
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_grouped_split_k(cuda, dtype, layout):
+    """Grouped launches whose grid fills less than one round split K: entry
+    z's partials follow entry z-1's in the workspace and the reduction finds
+    each entry's C through the table (swapped operands in column-major).
+    Run plain, with C off 16-byte alignment, and with the ReLU epilogue, with
+    ld padding around each window."""
+    import sushiblas_amd as sbx
+    code = sbx.F32 if dtype == np.float32 else sbx.F64
+    for m, n, k, count in ((128, 128, 4096, 8), (300, 200, 5000, 3)):
+        lda, ldb, ldc = (k, n, n) if layout == 0 else (m, k, m)
+        name = sbx.gemm_select(code, layout, 0, 0, m, n, k, lda, ldb, ldc, batch=count)
+        print(f"grouped split case {np.dtype(dtype).name} layout={layout} {m}x{n}x{k} "
+              f"x{count} -> {name}", flush=True)
+        assert "+splitk" in name, name
+        _grouped(cuda, dtype, layout, 0, 0, m, n, k, 1.0, 0.5, count, pad=(3, 5, 7))
+        _grouped(cuda, dtype, layout, 1, 1, m, n, k, -0.75, 0.0, count, misalign=True,
+                 pad=(1, 2, 3))
+        _grouped(cuda, dtype, layout, 0, 1, m, n, k, 1.5, -1.0, count, epilogue=1, pad=(0, 0, 4))

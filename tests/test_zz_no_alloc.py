@@ -147,3 +147,53 @@ def test_noalloc_split_batch_two_calls(cuda):
             w = want[b * str_c:(b + 1) * str_c].reshape(m, n)
             g = got[b * str_c:(b + 1) * str_c].reshape(m, n)
             assert oracle.rel_fro_err(g, w) <= TOL[np.float32], b
+
+
+def test_noalloc_concurrent_host_threads_one_stream(cuda):
+    """Six host threads share one stream and call sbx_gemm_ex_noalloc on two
+    split shapes in alternation.  Each call's partial kernel and reduction
+    must be enqueued back to back (the per-GPU scratch lock): were another
+    thread's partial kernel to land between them, the reduction would sum
+    that call's partials and return wrong values.  Every result is checked
+    against the oracle."""
+    import threading
+    import torch
+    import sushiblas_amd as sbx
+    shapes = [(1536, 1536, 1024), (384, 320, 3000)]
+    data = []
+    for i, (m, n, k) in enumerate(shapes):
+        name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+        print(f"noalloc threads case {m}x{n}x{k} -> {name}", flush=True)
+        assert "+splitk" in name, name
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 30 + i)
+        want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+        data.append((m, n, k, torch.from_numpy(A).to(cuda), lda, torch.from_numpy(B).to(cuda),
+                     ldb, ldc, want))
+    nthreads = 6
+    outs = [[torch.full((d[0] * d[1],), float("nan"), device=cuda) for _ in range(nthreads)]
+            for d in data]
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        try:
+            for rep in range(4):
+                for j in ((t + rep) % 2, (t + rep + 1) % 2):
+                    m, n, k, dA, lda, dB, ldb, ldc, _ = data[j]
+                    sbx.gemm_ex_noalloc(sbx.F32, 0, 0, 0, m, n, k, 1.0, dA, lda, 0, dB, ldb, 0,
+                                        0.0, outs[j][t], ldc, 0, stream=stream)
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nthreads)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    stream.synchronize()
+    assert not errors, errors
+    for (m, n, k, _, _, _, _, ldc, want), group in zip(data, outs):
+        for t, o in enumerate(group):
+            err = normwise(0, o.cpu().numpy(), want, m, n, ldc)
+            assert err <= TOL[np.float32], (m, n, k, t, err)
