@@ -28,9 +28,15 @@ Printed as one JSON line.  Besides the contract fields it carries:
                    patterns (microseconds per batch, one lane vs four)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-also]
-                       [--cpu-seconds S] [--no-cpu] [--no-vendor]
+                       [--cpu-seconds S] [--no-cpu] [--no-vendor] [--probe]
        python bench.py --only <also key>     (one secondary workload, for profiling)
        python bench.py --calibrate-copy      (1 GiB copy, the PMC byte reference)
+       python bench.py --probe --k-sweep     (512 x 512 x K on the small-problem kernel)
+
+--probe runs everything on the probe build of the library, whose GEMM kernels
+stamp the shader clock counter and a constant-rate counter per workgroup: the
+GEMM configs then also report, for the dispatches of their timed loop, the
+clock, the span and the MFMA busy fraction (no profiler, no serialisation).
 """
 import argparse
 import json
@@ -64,6 +70,14 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (torch copy_) a few "
                          "times: the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--probe", action="store_true",
+                    help="run on the probe build (lib/libsbx_probe.so): the GEMM configs "
+                         "also report the clock, loop span and MFMA busy of every timed "
+                         "dispatch from per-workgroup clock stamps (no serialisation)")
+    ap.add_argument("--k-sweep", action="store_true",
+                    help="with --probe: time 512 x 512 x K on the small-problem kernel for "
+                         "K = 512 ... 4096 (and K < 512 on its 4-wave form) and fit time = "
+                         "intercept + slope * K")
     return ap.parse_args()
 
 
@@ -79,9 +93,69 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n * 4, "dispatches": 3}), flush=True)
 
 
-def time_launches(fn, steps, warmup, min_warm_s=0.0):
+PROBE = False  # --probe: record per-workgroup clock stamps of the timed dispatches
+PROBE_BLOCKS = 4096  # workgroups per dispatch whose stamps are kept
+
+
+PROBE_POINTS = 4  # stamp points per workgroup (SBX_PROBE_POINTS)
+
+
+def probe_summary(t, ndisp, flops, dtype, call_ms, khz, cus):
+    """Clock, loop span and MFMA busy of the timed dispatches, from the probe
+    build's per-workgroup stamps (see sushiblas_amd/csrc/sbx_probe.h).
+
+    t: the stamp ring as uint64, ring x PROBE_BLOCKS x PROBE_POINTS x 2
+    (core cycles, real-time ticks at `khz`); unused entries are 0.  Per
+    dispatch: clock = median over workgroups of core cycles / real time
+    between the first and last stamp; span = last workgroup's last stamp -
+    first workgroup's entry; MFMA busy = flops / (MFMA flop per cycle of the
+    chip x clock x span).  `mfma_busy_of_call` uses the event-timed call time
+    instead of the span (it includes the epilogue and launch gaps)."""
+    import numpy as np
+    if khz <= 0 or ndisp <= 0:
+        return None
+    per_clk = (256 if dtype == "f32" else 128) * cus  # dense MFMA flop per cycle, MI355X
+    t = np.asarray(t).reshape(-1, PROBE_BLOCKS, PROBE_POINTS, 2).astype(np.float64)
+    rows = []
+    for d in range(min(ndisp, t.shape[0])):
+        x = t[d]
+        live = x[:, 0, 1] > 0
+        if not live.any():
+            continue
+        x = x[live]
+        last = 3 if (x[:, 3, 1] > 0).all() else 1  # small-problem kernel: 4 points
+        cyc = x[:, last, 0] - x[:, 0, 0]
+        rt = (x[:, last, 1] - x[:, 0, 1]) / (khz * 1e3)  # seconds
+        ok = rt > 0
+        clock = float(np.median(cyc[ok] / rt[ok])) / 1e9
+        span = (x[:, last, 1].max() - x[:, 0, 1].min()) / (khz * 1e3)
+        rows.append((clock, span * 1e6, float(np.median(cyc)), x))
+    if not rows:
+        return None
+    clocks = np.array([r[0] for r in rows])
+    spans = np.array([r[1] for r in rows])
+    c_med, s_med = float(np.median(clocks)), float(np.median(spans))
+    out = {"dispatches": len(rows), "clock_ghz": round(c_med, 3),
+           "clock_ghz_min": round(float(clocks.min()), 3),
+           "clock_ghz_max": round(float(clocks.max()), 3),
+           "span_us": round(s_med, 2), "wg_cycles": round(float(np.median([r[2] for r in rows]))),
+           "mfma_busy_span": round(flops / (per_clk * c_med * 1e9 * s_med * 1e-6), 4),
+           "mfma_busy_of_call": round(flops / (per_clk * c_med * 1e9 * call_ms * 1e-3), 4)}
+    x = rows[len(rows) // 2][3]
+    if (x[:, 3, 1] > 0).all():  # small-problem kernel: where a workgroup's time goes
+        us = lambda a, b: float(np.median(x[:, b, 1] - x[:, a, 1])) / (khz * 1e3) * 1e6
+        out["wg_us"] = {"issue_first_loads": round(us(0, 1), 3), "to_mfma_done": round(us(1, 2), 3),
+                        "reduce_and_store": round(us(2, 3), 3)}
+        out["launch_spread_us"] = round(float(x[:, 0, 1].max() - x[:, 0, 1].min()) /
+                                        (khz * 1e3) * 1e6, 3)
+    return out
+
+
+def time_launches(fn, steps, warmup, min_warm_s=0.0, probe=None):
     """Average device time per call of fn() over `steps` back-to-back calls,
-    measured with HIP events on the stream the kernels run on.
+    measured with HIP events on the stream the kernels run on.  With --probe
+    and a dict `probe` = {"flops": F, "dtype": "f32"|"f64"}, the timed
+    dispatches' stamps are recorded and probe["out"] gets probe_summary().
 
     `warmup` untimed calls come first; with min_warm_s > 0, more untimed calls
     follow until that much time has been spent warming up.  A GPU that sat
@@ -100,12 +174,29 @@ def time_launches(fn, steps, warmup, min_warm_s=0.0):
         torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    stamps = None
+    if PROBE and probe is not None:
+        import sushiblas_amd as sbx
+        stamps = torch.zeros(steps * PROBE_BLOCKS * PROBE_POINTS * 2, dtype=torch.int64,
+                             device="cuda")
+        torch.cuda.synchronize()
+        sbx.probe_set(stamps, PROBE_BLOCKS, steps)
     start.record()
     for _ in range(steps):
         fn()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms
+    ms = start.elapsed_time(end) / steps
+    if stamps is not None:
+        import numpy as np
+        import sushiblas_amd as sbx
+        ndisp = sbx.probe_dispatches()
+        sbx.probe_set(None, 0, 0)
+        probe["out"] = probe_summary(stamps.cpu().numpy().view(np.uint64), ndisp, probe["flops"],
+                                     probe["dtype"], ms, sbx.probe_wall_clock_khz(),
+                                     torch.cuda.get_device_properties(0).multi_processor_count)
+        del stamps
+    return ms  # ms
 
 
 def read_traffic(workload):
@@ -304,13 +395,16 @@ def run_config(dtype, layout, ta, tb, m, n, k, alpha, beta, seed, steps, warmup,
         step()
         torch.cuda.synchronize()
         host = host + (C.cpu().numpy(),)
-    ms = time_launches(step, steps, warmup, min_warm_s=0.25)
     flops = 2.0 * m * n * k
+    probe = {"flops": flops, "dtype": dtype}
+    ms = time_launches(step, steps, warmup, min_warm_s=0.25, probe=probe)
     tflops = flops / (ms * 1e-3) / 1e12
     nbytes = (m * k + k * n + m * n * (2 if beta != 0 else 1)) * A.element_size()
     out = {"kernel": name, "ms": round(ms, 4), "tflops": round(tflops, 3),
            "pct_peak": round(100 * tflops / PEAK[dtype], 2),
            "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    if probe.get("out"):
+        out["probe"] = probe["out"]
     if VENDOR and layout == 0:
         # the same problem through torch (the vendor BLAS) on the same
         # device buffers, into a separate output, timed the same way
@@ -474,8 +568,52 @@ def secondary_workloads(steps_arg, cpu_s=None):
     return w
 
 
+def k_sweep(steps):
+    """512 x 512 x K (fp32, row-major, no transpose, alpha = 1, beta = 0) on
+    the kernel the library picks (the small-problem kernel, 8 waves from
+    K = 512 and 4 below, up to about K = 1800), with the probe build's stamps:
+    event-timed call time, the dispatch's span and the workgroups' phases;
+    time = intercept + slope * K fitted over each small-kernel form's rows."""
+    import numpy as np
+    import torch
+    import sushiblas_amd as sbx
+    m = n = 512
+    rows = []
+    for k in (64, 128, 192, 256, 384, 512, 640, 768, 1024, 1280, 1536, 1792):
+        A = torch.empty(m * k, dtype=torch.float32, device="cuda")
+        B = torch.empty(k * n, dtype=torch.float32, device="cuda")
+        C = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+        sbx.fill_uniform(A, SEED + 1, 0)
+        sbx.fill_uniform(B, SEED + 1, 1)
+
+        def step():
+            sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0)
+
+        probe = {"flops": 2.0 * m * n * k, "dtype": "f32"}
+        ms = time_launches(step, steps, 5, min_warm_s=0.25, probe=probe)
+        rows.append({"k": k, "kernel": sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n),
+                     "us": round(ms * 1e3, 3), "probe": probe.get("out")})
+        del A, B, C
+    fits = {}
+    for form, name in (("8wave", "mfma_f32_32x32_ksplit8"), ("4wave", "mfma_f32_32x32_ksplit4")):
+        pts = [r for r in rows if r["kernel"] == name and r["probe"]]
+        if len(pts) < 2:
+            continue
+        ks = np.array([r["k"] for r in pts], dtype=np.float64)
+        fit = {"k": [r["k"] for r in pts]}
+        for key, ys in (("call_us", [r["us"] for r in pts]),
+                        ("span_us", [r["probe"]["span_us"] for r in pts])):
+            slope, icpt = np.polyfit(ks, np.array(ys), 1)
+            fit[key] = {"intercept_us": round(float(icpt), 3), "us_per_k": round(float(slope), 6)}
+        fits[form] = fit
+    return {"workload": "fp32 512 x 512 x K sweep (small-problem kernel)", "rows": rows,
+            "fit": fits,
+            "mfma_floor_us_per_k": round(2.0 * m * n / (256 * torch.cuda.get_device_properties(0)
+                                                        .multi_processor_count * 2.4e9) * 1e6, 6)}
+
+
 def main():
-    global VENDOR
+    global VENDOR, PROBE
     args = parse()
     VENDOR = not args.no_vendor
     if args.gpus != 1:
@@ -484,6 +622,18 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.probe:
+        import sushiblas_amd as sbx
+        PROBE = True
+        sbx.use_probe_library()
+    if args.k_sweep:
+        if not args.probe:
+            print("--k-sweep needs --probe", file=sys.stderr)
+            sys.exit(2)
+        import sushiblas_amd as sbx
+        sbx.lib()
+        print(json.dumps(k_sweep(max(args.steps, 20))), flush=True)
         return
     if args.only:
         import sushiblas_amd as sbx
@@ -525,8 +675,9 @@ def main():
     def step():
         sbx.sgemm(0, 0, 0, m, n, k, alpha, A, k, B, n, beta, C, n)
 
-    ms = time_launches(step, args.steps, args.warmup)
     flops = 2.0 * m * n * k
+    probe = {"flops": flops, "dtype": "f32"}
+    ms = time_launches(step, args.steps, args.warmup, probe=probe)
     value = flops / (ms * 1e-3) / 1e12
     traffic = read_traffic("headline")
     vendor = None if args.no_vendor else vendor_headline(A, B, C, m, n, k, alpha, beta,
@@ -553,6 +704,9 @@ def main():
     }
     if vendor is not None:
         result["vendor"] = vendor
+    if PROBE:
+        result["library"] = "probe build (lib/libsbx_probe.so): per-workgroup clock stamps"
+        result["probe"] = probe.get("out")
     if need_host:
         del A, B
         torch.cuda.empty_cache()

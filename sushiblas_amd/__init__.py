@@ -17,6 +17,9 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsbx.so")
+# The probe build of the same sources (csrc/sbx_probe.h): per-workgroup clock
+# stamps for measurements; use_probe_library() selects it before first use.
+PROBE_LIB_PATH = os.path.join(_HERE, "lib", "libsbx_probe.so")
 
 F32, F64 = 0, 1
 ALGO_AUTO, ALGO_GENERIC, ALGO_MFMA, ALGO_MFMA_TILE, ALGO_MFMA_SMALL = 0, 1, 2, 3, 4
@@ -40,6 +43,16 @@ def build(force: bool = True, jobs: int = 8) -> None:
     res = subprocess.run(args, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError("building libsbx.so failed:\n" + res.stdout[-4000:])
+
+
+def use_probe_library() -> None:
+    """Load lib/libsbx_probe.so instead of lib/libsbx.so: the same kernels
+    plus per-workgroup clock stamps (probe_set, probe_dispatches).  Must be
+    called before the first lib() call."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != PROBE_LIB_PATH:
+        raise RuntimeError("use_probe_library() after the product library was loaded")
+    LIB_PATH = PROBE_LIB_PATH
 
 
 def lib() -> ctypes.CDLL:
@@ -111,8 +124,33 @@ def lib() -> ctypes.CDLL:
                                   ctypes.c_double]
     L.sbx_version.restype = ctypes.c_char_p
     L.sbx_version.argtypes = []
+    if LIB_PATH == PROBE_LIB_PATH:
+        L.sbx_probe_set.restype = i32
+        L.sbx_probe_set.argtypes = [vp, i64, i64]
+        L.sbx_probe_dispatches.restype = i64
+        L.sbx_probe_dispatches.argtypes = []
+        L.sbx_probe_wall_clock_khz.restype = i64
+        L.sbx_probe_wall_clock_khz.argtypes = []
     _lib = L
     return L
+
+
+PROBE_POINTS = 4  # SBX_PROBE_POINTS
+
+
+def probe_set(buf, blocks: int, ring: int) -> None:
+    """Start recording stamps into `buf` (a uint64/int64 device tensor of
+    ring * blocks * PROBE_POINTS * 2 elements; None stops).  Probe build only."""
+    _check(lib().sbx_probe_set(_ptr(buf), blocks if buf is not None else 0,
+                               ring if buf is not None else 0), "sbx_probe_set")
+
+
+def probe_dispatches() -> int:
+    return int(lib().sbx_probe_dispatches())
+
+
+def probe_wall_clock_khz() -> int:
+    return int(lib().sbx_probe_wall_clock_khz())
 
 
 def _status_text(status: int) -> str:

@@ -211,7 +211,47 @@ struct GemmArgs {
     // Host side only: which operand the launch loads non-temporally (0
     // none, 1 A, 2 B), picking the kernel's STREAM variant.
     int stream_op;
+#ifdef SBX_PROBE
+    // Probe build only: per-workgroup timestamps of this dispatch (see
+    // ProbeClock), for workgroups [0, stamp_blocks) of batch entry 0.
+    unsigned long long* stamps;
+    int stamp_blocks;
+#endif
 };
+
+// ---------------------------------------------------------------------------
+// Probe build (lib/libsbx_probe.so, compiled with SBX_PROBE; the product
+// library has none of this): wave 0 of a workgroup reads the shader clock
+// counter (s_memtime, core cycles) and the constant-rate real-time counter
+// (s_memrealtime) at up to kStampPoints points of the kernel and stores each
+// pair at once (nothing stays live across the k loop), so that the host can
+// derive the clock and the busy cycles of every dispatch of a back-to-back
+// timed loop without serialising it (counter collection by a profiler runs
+// dispatches one at a time).
+// ---------------------------------------------------------------------------
+constexpr int kStampPoints = 4;
+
+template <typename T>
+__device__ inline void probe_mark(const GemmArgs<T>& p, int point)
+{
+#ifdef SBX_PROBE
+    // A branch on a wave-uniform condition (wave 0, read into a scalar
+    // register): on a per-lane one the compiler treats the kernel's later
+    // values as divergent and builds its buffer descriptors in VGPRs.  Every
+    // lane of wave 0 then stores the same 16 bytes.
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    if (!p.stamps || wave != 0 || blockIdx.z != 0 || blockIdx.x >= (unsigned)p.stamp_blocks)
+        return;
+    unsigned long long* d = p.stamps + ((size_t)blockIdx.x * kStampPoints + point) * 2;
+    const unsigned long long c = __builtin_amdgcn_s_memtime();
+    const unsigned long long r = __builtin_amdgcn_s_memrealtime();
+    d[0] = c;
+    d[1] = r;
+#else
+    (void)p;
+    (void)point;
+#endif
+}
 
 // Operand and result bases of batch entry z.
 template <typename T>
@@ -765,6 +805,7 @@ gemm_mfma_kernel(GemmArgs<T> p)
     if constexpr (PF > 3) issue(Int<3>{}, kt0 + 3);
     __syncthreads();
     read_frags(Int<0>{}, 0, 0);
+    probe_mark(p, 0);  // start of the k loop (after the prologue's first tile)
 
     constexpr std::false_type kNo{};
     constexpr std::true_type kYes{};
@@ -826,6 +867,8 @@ gemm_mfma_kernel(GemmArgs<T> p)
             if (kt + 4 < nk) step(Int<4 % PF>{}, kt + 4, cur, kYes, kNo);
         }
     }
+
+    probe_mark(p, 1);  // end of the k loop
 
     // ---- epilogue ----
     // Whole tile: C = alpha*acc + beta*C (C is not read when beta == 0).

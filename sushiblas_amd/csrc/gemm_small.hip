@@ -106,6 +106,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     constexpr int PART = NB * NB * NACC * 64;  // one wave's partial tile
     static_assert(PART == kTile * kTile, "a wave's blocks cover the tile once");
     __shared__ T red[NW * PART];  // the waves' partial tiles
+    probe_mark(p, 0);  // kernel entry
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // uniform per wave, and known to be: the buffer descriptors built from
@@ -173,6 +174,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     int k0 = 8 * g0;
     const int n = (ke - k0 + 31) / 32;
     if (n > 0) issue(0, k0);
+    probe_mark(p, 1);  // first stage's loads issued
     int done = 0;  // stages consumed
     for (; done + 2 < n; done += 2) {
         issue(1, k0 + 32);
@@ -188,6 +190,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     } else if (n - done == 1) {
         mma(0);
     }
+    probe_mark(p, 2);  // this wave's MFMAs issued
 
     // partial tiles -> LDS, element (bi, bj, r, lane) at ((bi*NB + bj)*NACC + r)*64 + lane
 #pragma unroll
@@ -218,6 +221,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
             *cp = p.relu ? relu_of(v) : v;
         }
     }
+    probe_mark(p, 3);  // C stores issued
 }
 
 }  // namespace

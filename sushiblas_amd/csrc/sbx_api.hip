@@ -17,6 +17,9 @@
 #include "../../include/sbx.h"
 #include "gemv.hpp"
 #include "launch.hpp"
+#ifdef SBX_PROBE
+#include "sbx_probe.h"
+#endif
 
 namespace sbx {
 
@@ -605,6 +608,29 @@ int stream_operand(const Problem& p, int tiles_m, int tiles_n)
     return 0;
 }
 
+#ifdef SBX_PROBE
+// Probe build: the timestamp ring that sbx_probe_set installs, and the slot of
+// the next GEMM dispatch.
+static_assert(SBX_PROBE_POINTS == kStampPoints, "probe header and kernels agree");
+std::mutex g_probe_mu;
+unsigned long long* g_probe_buf = nullptr;
+int64_t g_probe_blocks = 0, g_probe_ring = 0, g_probe_count = 0;
+
+template <typename T>
+void probe_assign(GemmArgs<T>& a)
+{
+    std::lock_guard<std::mutex> g(g_probe_mu);
+    if (!g_probe_buf) {
+        a.stamps = nullptr;
+        a.stamp_blocks = 0;
+        return;
+    }
+    a.stamps = g_probe_buf + (size_t)(g_probe_count++ % g_probe_ring) * (size_t)g_probe_blocks *
+                                 kStampPoints * 2;
+    a.stamp_blocks = (int)g_probe_blocks;
+}
+#endif
+
 // A caller-provided split workspace: the allocation-free entry point's
 // per-device scratch.  `launch_mu` plays the part of Workspace::launch_mu:
 // it is held from handing out the scratch until the split kernels are
@@ -740,8 +766,11 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             // GROUP_M: the height of the tile-column walk.  An XCD's 64
             // resident 256x128 workgroups then cover 4 x 16 tiles (1024 rows
             // of A, 2048 columns of B), which fetches 2.3 GB from beyond L2
-            // at 8192^3 against 3.4 GB for 8 x 8, in the same time.
-            const int gm = cfg == F32_256x128 ? 4 : 8;
+            // at 8192^3 against 3.4 GB for 8 x 8, in the same time.  The
+            // fp64 128^2 tile likewise: 12.9 GB from beyond L2 at 8192^3
+            // against 13.5 GB for 8 (19.3 for 2, 22.6 for 16), same time;
+            // its SYRK 9.1 against 9.4 GB.
+            const int gm = cfg == F32_256x128 || cfg == F64_128x128 ? 4 : 8;
             a.group_m = a.tiles_m < gm ? a.tiles_m : gm;
             a.c_vec = p.ldc % (16 / (int64_t)sizeof(T)) == 0 && (uintptr_t)a.C % 16 == 0 &&
                       (p.batch <= 1 || p.str_c % (16 / (int64_t)sizeof(T)) == 0);
@@ -754,6 +783,9 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.table = p.table ? p.table + 3 * b0 : nullptr;
             a.table_swap = p.table_swap;
             a.stream_op = stream_operand(p, a.tiles_m, a.tiles_n);
+#ifdef SBX_PROBE
+            probe_assign(a);
+#endif
             // A (m x k) is k-contiguous iff not transposed, B (k x n) iff transposed
             e = launch_cfg(cfg, a, !p.ta, p.tb != 0, p, nb, stream);
         }
@@ -1262,5 +1294,35 @@ int sbx_fill_normal(void* stream, int dtype, void* out, int64_t n, uint64_t seed
 }
 
 const char* sbx_version(void) { return "sushiblas_amd 0.1.0 (gfx950)"; }
+
+#ifdef SBX_PROBE
+int sbx_probe_set(void* buf, int64_t blocks, int64_t ring)
+{
+    if (buf && (blocks <= 0 || blocks > (int64_t)1 << 20 || ring <= 0 ||
+                (uintptr_t)buf % sizeof(unsigned long long)))
+        return SBX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> g(sbx::g_probe_mu);
+    sbx::g_probe_buf = static_cast<unsigned long long*>(buf);
+    sbx::g_probe_blocks = buf ? blocks : 0;
+    sbx::g_probe_ring = buf ? ring : 0;
+    sbx::g_probe_count = 0;
+    return SBX_OK;
+}
+
+int64_t sbx_probe_dispatches(void)
+{
+    std::lock_guard<std::mutex> g(sbx::g_probe_mu);
+    return sbx::g_probe_count;
+}
+
+int64_t sbx_probe_wall_clock_khz(void)
+{
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+        return 0;
+    return khz;
+}
+#endif
 
 }  // extern "C"
