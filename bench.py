@@ -74,6 +74,15 @@ def parse():
                     help="run on the probe build (lib/libsbx_probe.so): the GEMM configs "
                          "also report the clock, loop span and MFMA busy of every timed "
                          "dispatch from per-workgroup clock stamps (no serialisation)")
+    ap.add_argument("--regret", type=int, default=None, metavar="SEED",
+                    help="time the kernel-selection pick against every candidate plan on the "
+                         "seeded shape list (regret_shapes) and report the regret")
+    ap.add_argument("--regret-count", type=int, default=60,
+                    help="shapes in the --regret list")
+    ap.add_argument("--regret-syrk", type=int, default=0,
+                    help="SYRK shapes in the --regret list (regret_syrk_shapes)")
+    ap.add_argument("--regret-full", action="store_true",
+                    help="keep every plan's measured and predicted time in the --regret rows")
     ap.add_argument("--k-sweep", action="store_true",
                     help="with --probe: time 512 x 512 x K on the small-problem kernel for "
                          "K = 512 ... 4096 (and K < 512 on its 4-wave form) and fit time = "
@@ -612,6 +621,170 @@ def k_sweep(steps):
                                                         .multi_processor_count * 2.4e9) * 1e6, 6)}
 
 
+def regret_shapes(seed, count):
+    """A seeded list of GEMM problems for judging the kernel-selection model:
+    fp32 (70 %) and fp64, both layouts, all four transposes; unbatched with
+    m, n, k log-uniform in [64, 8192], or (a quarter) strided batches of 2-64
+    entries with sides in [32, 1024]; resampled until 2mnk*batch lies in
+    [1e8, 4e11] flop (each call about 2 us to 5 ms)."""
+    import numpy as np
+    rng = np.random.RandomState(seed)
+    out = []
+    while len(out) < count:
+        dtype = "f32" if rng.rand() < 0.7 else "f64"
+        layout, ta, tb = (int(x) for x in rng.randint(0, 2, 3))
+        if rng.rand() < 0.25:
+            batch = int(rng.choice([2, 4, 8, 16, 32, 64]))
+            m, n, k = (int(np.exp(rng.uniform(np.log(32), np.log(1024)))) for _ in range(3))
+        else:
+            batch = 1
+            m, n, k = (int(np.exp(rng.uniform(np.log(64), np.log(8192)))) for _ in range(3))
+        flops = 2.0 * m * n * k * batch
+        if not 1e8 <= flops <= 4e11:
+            continue
+        out.append((dtype, layout, ta, tb, m, n, k, batch))
+    return out
+
+
+def regret_syrk_shapes(seed, count):
+    """A seeded list of SYRK problems (the triangle's plans): fp32 (70 %) and
+    fp64, both layouts, triangles and transposes; n and k log-uniform in
+    [64, 8192], resampled until n^2 k lies in [1e8, 4e11] flop."""
+    import numpy as np
+    rng = np.random.RandomState(seed + 7919)
+    out = []
+    while len(out) < count:
+        dtype = "f32" if rng.rand() < 0.7 else "f64"
+        layout, upper, trans = (int(x) for x in rng.randint(0, 2, 3))
+        n, k = (int(np.exp(rng.uniform(np.log(64), np.log(8192)))) for _ in range(2))
+        if not 1e8 <= float(n) * n * k <= 4e11:
+            continue
+        out.append((dtype, layout, upper, trans, n, k))
+    return out
+
+
+def _time_plans(call, plans):
+    """Times of the pick (call(None)) and of every named plan, in ms: each the
+    faster of two passes (plans in order, then reversed) of back-to-back
+    calls, about 2 ms of the pick's work per timing."""
+    import torch
+    import sushiblas_amd as sbx
+    call(None)
+    torch.cuda.synchronize()
+    t0 = time_launches(lambda: call(None), 3, 1)
+    reps = int(max(3, min(200, 2.0 / max(t0, 1e-3))))
+    names = [None] + [pn for pn, _ in plans]
+    times = {}
+    for order in (names, names[::-1]):
+        for pn in order:
+            try:
+                ms = time_launches(lambda: call(pn), reps, 2)
+            except sbx.SbxError:
+                continue
+            times[pn] = min(times.get(pn, float("inf")), ms)
+    return times
+
+
+def _regret_row(r, pick, plans, times, flops, full):
+    best = min((t, pn) for pn, t in times.items() if pn is not None)
+    r.update({"pick": pick, "pick_us": round(times[None] * 1e3, 2), "best": best[1],
+              "best_us": round(best[0] * 1e3, 2), "regret": round(times[None] / best[0] - 1.0, 4),
+              "plans": len(times) - 1,
+              "pick_tflops": round(flops / (times[None] * 1e-3) / 1e12, 2)})
+    if full:  # every plan's measured and predicted microseconds
+        pred = dict(plans)
+        r["times"] = {pn: [round(t * 1e3, 3), pred[pn]] for pn, t in times.items()
+                      if pn is not None}
+    print(json.dumps(r), file=sys.stderr, flush=True)
+    return r
+
+
+def _regret_summary(rows):
+    import numpy as np
+    if not rows:
+        return None
+    reg = np.array([r["regret"] for r in rows])
+    return {"shapes": len(rows), "mean_regret": round(float(reg.mean()), 4),
+            "median_regret": round(float(np.median(reg)), 4),
+            "p90_regret": round(float(np.percentile(reg, 90)), 4),
+            "max_regret": round(float(reg.max()), 4), "within_2pct": int((reg <= 0.02).sum()),
+            "within_10pct": int((reg <= 0.10).sum())}
+
+
+def regret(seed, count, full=False, syrk_count=0):
+    """For each shape of regret_shapes(seed, count) and
+    regret_syrk_shapes(seed, syrk_count): the time of the pick (sbx_gemm_ex,
+    algo AUTO; sbx_{s,d}syrk_strided_batched) and of every plan the heuristics
+    weigh (sbx_gemm_plans / sbx_syrk_plans, run through sbx_gemm_ex_plan /
+    sbx_syrk_ex_plan); regret = pick / fastest - 1.  full: keep every plan's
+    measured and predicted time in its row (for fitting the model)."""
+    import torch
+    import sushiblas_amd as sbx
+    rows, srows = [], []
+    for si, (dtype, layout, ta, tb, m, n, k, batch) in enumerate(regret_shapes(seed, count)):
+        code = sbx.F32 if dtype == "f32" else sbx.F64
+        tdt = torch.float32 if dtype == "f32" else torch.float64
+        rows_a = m if (layout == 0) == (not ta) else k
+        cols_a = k if (layout == 0) == (not ta) else m
+        rows_b = k if (layout == 0) == (not tb) else n
+        cols_b = n if (layout == 0) == (not tb) else k
+        rows_c, cols_c = (m, n) if layout == 0 else (n, m)
+        lda, ldb, ldc = cols_a, cols_b, cols_c  # packed: the stored row length
+        sa, sb, sc = rows_a * lda, rows_b * ldb, rows_c * ldc
+        A = torch.empty(sa * batch, dtype=tdt, device="cuda")
+        B = torch.empty(sb * batch, dtype=tdt, device="cuda")
+        C = torch.zeros(sc * batch, dtype=tdt, device="cuda")
+        sbx.fill_uniform(A, SEED + si, 0)
+        sbx.fill_uniform(B, SEED + si, 1)
+        pick = sbx.gemm_select(code, layout, ta, tb, m, n, k, lda, ldb, ldc, batch=batch)
+        plans = sbx.gemm_plans(code, layout, ta, tb, m, n, k, lda, ldb, ldc, batch)
+
+        def call(plan):
+            if plan is None:
+                sbx.gemm_ex(code, layout, ta, tb, m, n, k, 1.0, A, lda, sa, B, ldb, sb, 0.0, C,
+                            ldc, sc, batch)
+            else:
+                sbx.gemm_ex_plan(code, layout, ta, tb, m, n, k, 1.0, A, lda, sa, B, ldb, sb, 0.0,
+                                 C, ldc, sc, batch, plan)
+
+        times = _time_plans(call, plans)
+        r = {"op": "gemm", "dtype": dtype, "layout": layout, "ta": ta, "tb": tb, "m": m, "n": n,
+             "k": k, "batch": batch}
+        rows.append(_regret_row(r, pick, plans, times, 2.0 * m * n * k * batch, full))
+        del A, B, C
+        torch.cuda.empty_cache()
+    for si, (dtype, layout, upper, trans, n, k) in enumerate(regret_syrk_shapes(seed, syrk_count)):
+        code = sbx.F32 if dtype == "f32" else sbx.F64
+        tdt = torch.float32 if dtype == "f32" else torch.float64
+        lda = (k if not trans else n) if layout == 0 else (n if not trans else k)
+        A = torch.empty(n * k, dtype=tdt, device="cuda")
+        C = torch.zeros(n * n, dtype=tdt, device="cuda")
+        sbx.fill_uniform(A, SEED + 500 + si, 0)
+        pick = sbx.syrk_select(code, layout, upper, trans, n, k, lda, n)
+        plans = sbx.syrk_plans(code, layout, upper, trans, n, k, lda, n)
+
+        def call(plan):
+            if plan is None:
+                sbx.syrk(code, layout, upper, trans, n, k, 1.0, A, lda, 0, 0.0, C, n, 0)
+            else:
+                sbx.syrk_ex_plan(code, layout, upper, trans, n, k, 1.0, A, lda, 0, 0.0, C, n, 0,
+                                 1, plan)
+
+        times = _time_plans(call, plans)
+        r = {"op": "syrk", "dtype": dtype, "layout": layout, "upper": upper, "trans": trans,
+             "n": n, "k": k}
+        srows.append(_regret_row(r, pick, plans, times, float(n) * n * k, full))
+        del A, C
+        torch.cuda.empty_cache()
+    worst = sorted(rows + srows, key=lambda r: -r["regret"])[:8]
+    if not full:
+        worst = [{key: v for key, v in r.items() if key != "times"} for r in worst]
+    return {"workload": f"kernel-selection regret, regret_shapes({seed}, {count}) and "
+                        f"regret_syrk_shapes({seed}, {syrk_count})",
+            "gemm": _regret_summary(rows), "syrk": _regret_summary(srows),
+            "worst": worst, "rows": rows + srows}
+
+
 def main():
     global VENDOR, PROBE
     args = parse()
@@ -627,6 +800,12 @@ def main():
         import sushiblas_amd as sbx
         PROBE = True
         sbx.use_probe_library()
+    if args.regret is not None:
+        import sushiblas_amd as sbx
+        sbx.lib()
+        print(json.dumps(regret(args.regret, args.regret_count, args.regret_full,
+                                args.regret_syrk)), flush=True)
+        return
     if args.k_sweep:
         if not args.probe:
             print("--k-sweep needs --probe", file=sys.stderr)

@@ -219,10 +219,47 @@ int sbx_gemm_select_batched(int dtype, int layout, int transA, int transB, int64
                             int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
                             char* name, size_t cap);
 
+/* The plans the tiling heuristics weigh for this (packed, as above) problem:
+ * one line "<plan name> <predicted microseconds>\n" per candidate kernel and
+ * k-split, in the names sbx_gemm_select reports (NUL-terminated, at most cap
+ * bytes; SBX_INVALID_ARGUMENT if they do not fit).  No counterpart in the
+ * reference: it serves measurements of the heuristics against every
+ * candidate (regret), with sbx_gemm_ex_plan. */
+int sbx_gemm_plans(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                   int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch, char* out,
+                   size_t cap);
+
+/* sbx_gemm_ex (algo = AUTO) with the named plan -- a name from sbx_gemm_plans
+ * or sbx_gemm_select -- instead of the heuristics' pick.  Same results as any
+ * plan within the tolerance.  SBX_INVALID_ARGUMENT for a name that is no
+ * plan, SBX_UNSUPPORTED for a plan the problem cannot use (another element
+ * type, offsets beyond the kernel's range, more k-ranges than its tail
+ * allows).  No counterpart in the reference (measurement hook, as above). */
+int sbx_gemm_ex_plan(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                     int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                     int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                     void* C, int64_t ldc, int64_t str_c, int64_t batch, const char* plan);
+
 /* The same for sbx_{s,d}syrk[_strided_batched] (single problem): the kernel
  * and split that would compute the triangle. */
 int sbx_syrk_select(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
                     int64_t lda, int64_t ldc, char* name, size_t cap);
+
+/* sbx_gemm_plans for a single SYRK problem: the plans (square tile configs
+ * over the triangle, unsplit and split) the heuristics weigh.  No counterpart
+ * in the reference (measurement hook, as above). */
+int sbx_syrk_plans(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
+                   int64_t lda, int64_t ldc, char* out, size_t cap);
+
+/* sbx_{s,d}syrk_strided_batched with the named plan (a name from
+ * sbx_syrk_plans or sbx_syrk_select) instead of the heuristics' pick; status
+ * as sbx_gemm_ex_plan (a config that is not a triangle's is
+ * SBX_UNSUPPORTED).  alpha and beta point to the element type's scalar.  No
+ * counterpart in the reference (measurement hook, as above). */
+int sbx_syrk_ex_plan(void* stream, int dtype, int layout, int upper, int trans, int64_t n,
+                     int64_t k, const void* alpha, const void* A, int64_t lda, int64_t str_a,
+                     const void* beta, void* C, int64_t ldc, int64_t str_c, int64_t batch,
+                     const char* plan);
 
 /* Human-readable text for a status code (static storage). */
 const char* sbx_status_string(int status);

@@ -112,9 +112,19 @@ def lib() -> ctypes.CDLL:
     L.sbx_gemm_select_batched.restype = i32
     L.sbx_gemm_select_batched.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, i64,
                                           ctypes.c_char_p, ctypes.c_size_t]
+    L.sbx_gemm_plans.restype = i32
+    L.sbx_gemm_plans.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, i64,
+                                 ctypes.c_char_p, ctypes.c_size_t]
+    L.sbx_gemm_ex_plan.restype = i32
+    L.sbx_gemm_ex_plan.argtypes = L.sbx_gemm_ex.argtypes[:-1] + [ctypes.c_char_p]
     L.sbx_syrk_select.restype = i32
     L.sbx_syrk_select.argtypes = [i32, i32, i32, i32, i64, i64, i64, i64, ctypes.c_char_p,
                                   ctypes.c_size_t]
+    L.sbx_syrk_plans.restype = i32
+    L.sbx_syrk_plans.argtypes = L.sbx_syrk_select.argtypes
+    L.sbx_syrk_ex_plan.restype = i32
+    L.sbx_syrk_ex_plan.argtypes = [vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, i64, vp, vp,
+                                   i64, i64, i64, ctypes.c_char_p]
     L.sbx_status_string.restype = ctypes.c_char_p
     L.sbx_status_string.argtypes = [i32]
     L.sbx_fill_uniform.restype = i32
@@ -267,6 +277,54 @@ def gemm_select(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc, batch=1) 
                                              lda, ldb, ldc, batch, buf, 128),
                "sbx_gemm_select_batched")
     return buf.value.decode()
+
+
+def _plan_lines(buf):
+    out = []
+    for line in buf.value.decode().splitlines():
+        name, us = line.split()
+        out.append((name, float(us)))
+    return out
+
+
+def gemm_plans(dtype, layout, transA, transB, m, n, k, lda, ldb, ldc, batch=1):
+    """The candidate plans the heuristics weigh: [(plan name, predicted us)]."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(lib().sbx_gemm_plans(dtype, layout, int(transA), int(transB), m, n, k, lda, ldb, ldc,
+                                batch, buf, len(buf)), "sbx_gemm_plans")
+    return _plan_lines(buf)
+
+
+def syrk_plans(dtype, layout, upper, trans, n, k, lda, ldc):
+    """The candidate plans the heuristics weigh for a SYRK: [(plan name, predicted us)]."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(lib().sbx_syrk_plans(dtype, layout, int(upper), int(trans), n, k, lda, ldc, buf,
+                                len(buf)), "sbx_syrk_plans")
+    return _plan_lines(buf)
+
+
+def syrk_ex_plan(dtype, layout, upper, trans, n, k, alpha, A, lda, str_a, beta, C, ldc, str_c,
+                 batch=1, plan="", stream=None) -> None:
+    """sbx_syrk_ex_plan: sbx_{s,d}syrk_strided_batched with a named plan."""
+    real = ctypes.c_float if dtype == F32 else ctypes.c_double
+    a = real(alpha)
+    b = real(beta)
+    st = lib().sbx_syrk_ex_plan(_stream(stream), dtype, int(layout), int(upper), int(trans), n, k,
+                                ctypes.byref(a), _ptr(A), lda, str_a, ctypes.byref(b), _ptr(C),
+                                ldc, str_c, batch, plan.encode())
+    _check(st, "sbx_syrk_ex_plan")
+
+
+def gemm_ex_plan(dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a, B, ldb, str_b,
+                 beta, C, ldc, str_c, batch=1, plan="", stream=None) -> None:
+    """sbx_gemm_ex_plan: sbx_gemm_ex with a named plan instead of the pick."""
+    real = ctypes.c_float if dtype == F32 else ctypes.c_double
+    a = real(alpha)
+    b = real(beta)
+    st = lib().sbx_gemm_ex_plan(_stream(stream), dtype, int(layout), int(transA), int(transB), m,
+                                n, k, ctypes.byref(a), _ptr(A), lda, str_a, _ptr(B), ldb, str_b,
+                                ctypes.byref(b), _ptr(C), ldc, str_c, batch, plan.encode())
+    _check(st, "sbx_gemm_ex_plan")
 
 
 def syrk_select(dtype, layout, upper, trans, n, k, lda, ldc) -> str:

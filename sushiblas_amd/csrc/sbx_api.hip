@@ -7,6 +7,7 @@
 
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
@@ -73,7 +74,7 @@ enum Cfg {
     F64_64x64,     // fp64 mid-size: 4 waves of 32x32
     F32_SMALL,     // small problems: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
     F64_SMALL,
-    F32_SMALL8,    // the same with 8 waves: at most one tile per CU and K >= 512
+    F32_SMALL8,    // the same with K cut over 8 waves
     GENERIC,
 };
 
@@ -104,8 +105,8 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Tile configurations worth modelling for a problem, the default first; cus
 // is the device's CU count (the round size of one-per-CU tiles).  *large is
 // set for the large-fp32 candidates, whose model adds an epilogue term.  At
-// most kMaxCands are written (the fp32 branch of mid-size shapes has six).
-constexpr int kMaxCands = 6;
+// most kMaxCands are written (the fp32 branch of mid-size shapes has seven).
+constexpr int kMaxCands = 7;
 int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out, bool* large)
 {
     *large = false;
@@ -118,8 +119,7 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         int c = 0;
         const int64_t t = cdiv(n, 256);
         if (t * (t + 1) / 2 >= cus) out[c++] = F32_256x256;
-        // three per CU before two: timed on 8 triangles (1000..8192), the
-        // pick is then within 2.6 % of the fastest (8.2 % the other way)
+        // the order breaks exact ties of the model only
         out[c++] = F32_128x128_O3;
         out[c++] = F32_128x128;
         return c;
@@ -188,6 +188,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         if (f32) out[c++] = F32_64x64;
     }
     out[c++] = f32 ? F32_SMALL : F64_SMALL;
+    // the 8-wave form cuts K over twice the waves: it shortens each wave's
+    // chain of dependent loads where few tiles share a CU (512^3: 6.45 ->
+    // 6.19 us, 256^2 x 4096: 37.6 -> 29.2 us)
+    if (f32) out[c++] = F32_SMALL8;
     return c;
 }
 
@@ -217,35 +221,33 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 }
 
 // ---------------------------------------------------------------------------
-// Kernel choice and split-K from a cost model fitted to measurements of these
-// kernels on MI355X: every candidate tile x split of 24 fp32 and 24 fp64
-// shapes (512^3 .. 4096^3, the ragged 4095x3001x2047 in all four transposes,
-// K from 300 to 8192); the model's pick is on average within 0.7 % of the
-// fastest measured candidate, and at most 7 % off (the same on 12 larger
-// fp32 shapes, 3072^3 .. 8192^2 x 4096, timed later):
-//   * a workgroup's work is w = 2*BM*BN*K_part / R, R = 0.55 TFLOP/s per CU
-//     (fp32; 0.275 fp64);
-//   * a config keeps P workgroups per CU (its waves per SIMD); a round of
-//     P*CUs workgroups takes P*w; a partial round whose busiest CU holds
-//     q < P workgroups takes q*w/e1, where e1 = 0.9 is what a CU achieves
-//     short of its co-resident partners;
-//   * the grid adds F = 4 us once (pipeline fill and the last epilogue; in
-//     between, co-resident workgroups hide each other's);
-//   * a split adds the reduction kernel and the partial round trip,
-//     G + (partial bytes the reduction reads) / W with G = 7.5 us and
-//     W = 6 TB/s;
-//   * the one-launch small-problem kernel (32x32 tiles, work w = 2*32*32*K
-//     each) takes 1.5 us + max(ceil(tiles / 2CUs) * w / Rs, ceil(tiles /
-//     CUs) * w / Rc), Rs = 0.21 and Rc = 0.31 TFLOP/s per CU for fp32,
-//     0.7 of those for fp64 (fitted on 26 more fp32 and 26 more fp64
-//     shapes from 64^3 to 2048x2048x256 and 40 random fp32 shapes from 300
-//     to 7000 per dimension; over all 148 shapes the pick is within 0.7 %
-//     of the fastest on average), times a factor for k-contiguous operands
-//     (see model_plan).
+// Kernel choice and split-K: the candidate plan (tile config x split) with
+// the least modelled time.  The model's constants were fitted (bounded least
+// squares on log time, robust loss) to every candidate plan of 323 problems
+// timed on MI355X, 14008 plan timings: bench.py's regret_shapes(seed, 70)
+// for seeds 101, 102 and 103 (fp32 and fp64, both layouts and all four
+// transposes, a quarter of them batched, 1e8 .. 4e11 flops), 24 SYRK
+// problems of regret_syrk_shapes(101, 24), and 89 fixed problems (the
+// benchmark's shapes, the selection tests' shapes: large, tall, wide and
+// long-K ones, batches of small ones, SYRK).  Fitted on two of the random
+// seeds and the fixed problems,
+// the pick on the third seed was on average 1.4-3.3 % slower than the
+// fastest plan.
+//   * a tile config keeps P workgroups per CU (its waves per SIMD); a
+//     workgroup's time is w = 2*BM*BN*K_part / (R * eff) + kTileSec +
+//     (C tile bytes) / kTileStoreBw, R per dtype, eff per config;
+//   * a round of P*CUs workgroups takes P*w; a partial round whose busiest
+//     CU holds q < P workgroups takes q*w/e1, e1 what a CU achieves short of
+//     its co-resident partners;
+//   * the grid adds F once (pipeline fill and the last epilogue; in between,
+//     co-resident workgroups hide each other's);
+//   * a split adds the reduction kernel and the partial round trip, G +
+//     (partial bytes the reduction reads) / W, and each part kPartSec;
+//   * the one-launch small-problem kernel is modelled on its own (see
+//     small_seconds).
 // Whole rounds run unsplit; only the tail (T mod P*CUs tiles, or all of them)
-// may be cut into s <= 32 k-ranges (at least 2 k tiles each; a part costs a
-// fixed kPartSec more).  A split is taken if predicted >= 2 %
-// faster, another tile shape if >= 3 % faster than the default.
+// may be cut into s k-ranges of at least two k tiles each, s from kSplitSet;
+// a split is taken if predicted >= 0.5 % faster than the fewer ranges before it.
 // Split partials live in a workspace cached per (device, stream): calls on
 // one stream are ordered, so they can share it; the first call that needs
 // more memory grows it (the only allocation on the GEMM path; outgrown
@@ -290,123 +292,175 @@ double rounds_time(int64_t units, double work, int64_t per_cu, int64_t cus, doub
     return t;
 }
 
-// The small-problem kernel: a workgroup alone on a CU computes at
-// kSmallRate (it waits on its loads); a second one beside it costs nothing
-// extra, and past that the CU's kSmallCuRate limits.  fp64 runs at
-// kSmallF64Rate of the fp32 rates.  Fitted on 26 fp32 and 26 fp64 small
-// shapes, 64^3 .. 2048x2048x256, and 40 random fp32 shapes, with the tile
-// kernels' splits as the alternatives: over those and the 56 larger shapes
-// the pick is within 0.7 % of the fastest on average.
-constexpr double kSmallRate = 0.21e12;
-constexpr double kSmallCuRate = 0.31e12;
-constexpr double kSmallF64Rate = 0.7;
-// fp64 past one tile per CU: the CU's throughput falls short of
-// kSmallF64Rate x kSmallCuRate (fp64 NN 576^3 took 19.5 us and 768^3 31.7,
-// 0.13-0.17 TFLOP/s per CU; the 64^2 tile 16.3 and 27.6)
-constexpr double kSmallF64CuRate = 0.52;
-// Its operand bytes at kSmallBw bound it too: a long reduction over a wide
-// operand streams (32 x 65536 x 4096: 283 us measured, 218 from the rates
-// alone -- 1.07 GB at 3.8 TB/s -- and 241 for the 64x256 tile).  The shapes
-// the rates were fitted on move too few bytes for this to bind.  A batch
-// of small problems streams its problems' own contiguous slabs faster, at
-// kSmallBwBatch (1024 x 32 x 32 x 512 read 138 MB in 22.4 us, 6.2 TB/s,
-// where 4 TB/s sent it to a tile kernel taking 36.5; the bound still keeps
-// 512 x 64^3 on the 64^2 tile, 9.7 against 11.1 us fp32, 11.4 against
-// 21.2 fp64).
-constexpr double kSmallBw = 4e12;
-constexpr double kSmallBwBatch = 5e12;
+// Fitted constants of the tile configs (per CU, seconds, bytes per second).
+constexpr double kRateF32 = 5.926e11;
+constexpr double kRateF64 = 2.964e11;
+constexpr double kGridSec = 4.409e-6;     // F
+constexpr double kReduceSec = 3.112e-6;   // G
+constexpr double kReduceBw = 3.711e12;    // W
+constexpr double kPartSec = 8.200e-7;
+constexpr double kTileSec = 7.824e-7;
+constexpr double kTileStoreBw = 2.2870e10;
+constexpr double kE1 = 0.9944;
 
-// Large fp32 shapes (epi set): a tile's epilogue moves its C tile, and the
-// CU's other workgroups hide only part of that time.  The model adds, per
-// whole tile, kEpiSec per byte of the C tile, times 12 for C rows that take
-// no vector access (single-element loads and stores), and per split part
-// kEpiSec per byte of its partial; both times 0.2 at three workgroups per
-// CU.  Fitted on 78 large shapes (K = 128 ... 8192, beta 0 and 0.5, every
-// large tile and split timed): the pick is within 0.8 % of the fastest on
-// average and 4.1 % at most, against 2.1 % and 30 % without the term
-// (8191 x 8190 x 128: 296 against 229 us).  It does not depend on beta, so
-// sbx_gemm_select names the pick for every beta.
-constexpr double kEpiSec = 0.01e-9;
-
-// Each split part also pays a fixed cost (its pipeline fill and its partial's
-// store).  Fitted on 36 mid-size shapes whose pick splits more than 8 ways
-// and 12 long-K shapes (256^2 x 65536 ...), every split 1-32 of the picked
-// tile timed: the split picked is 0.66 % from that tile's fastest on average
-// and 4.5 % at most (1.3 % and 17 % without the term).
-constexpr double kPartSec = 1e-6;
-
-// max_ws: the most split-partial bytes a plan may use (the allocation-free
-// entry point's scratch size; unlimited otherwise).
-Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi = false)
+// Relative MFMA rate of a tile config.  1 for the 128^2 tiles, which the
+// rates are quoted on, for the configs only tall, wide or large shapes reach,
+// and for the fp64 128x64 and 64x128 tiles, whose fitted factors (1.005,
+// 1.001) left the cross-validated regret unchanged when fixed at 1 (and
+// moved the fp64 8192^3 pick off the 128^2 tile, 14630 against 14400 us).
+double cfg_eff(Cfg c)
 {
-    if (c == F32_SMALL || c == F64_SMALL) {
-        // One launch, no split.  Its waves read operands straight from
-        // memory in the MFMA lane layout, so a k-contiguous operand is read
-        // as one 16-byte run per row per lane and touches many more cache
-        // lines per load than an x-contiguous one: measured against both
-        // operands x-contiguous on 10 shapes 512^3 .. 1152^3, A and B both
-        // k-contiguous took 1.15-1.29x (fp64 1.26-1.38x), A alone 1.03-1.07x
-        // (fp64 1.04-1.15x), B alone 1.0x (fp64 1.03-1.11x).  The model
-        // charges fp32 only the first (with A alone the tile kernels' picks
-        // were the slower ones: 896^3 27.9 against 23.8 us).
-        const double f = c == F64_SMALL ? kSmallF64Rate : 1.0;
-        const bool akc = !p.ta, bkc = p.tb;
-        const double lay = c == F64_SMALL ? (akc && bkc ? 1.3 : akc ? 1.12 : bkc ? 1.07 : 1.0)
-                                          : (akc && bkc ? 1.22 : 1.0);
-        const int64_t units = tile_count(p, c) * (p.batch > 1 ? p.batch : 1);
-        const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
-        const double lat = (double)cdiv(units, 2 * cus) * w / (kSmallRate * f);
-        const double thr = (double)cdiv(units, cus) * w /
-                           (kSmallCuRate * (c == F64_SMALL ? kSmallF64CuRate : 1.0));
-        const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
-        const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
-                             (double)(p.batch > 1 ? p.batch : 1);
-        const double stream = bytes / (p.batch > 1 ? kSmallBwBatch : kSmallBw);
-        const double compute = (lat > thr ? lat : thr) * lay;
-        const double t = 1.5e-6 + (compute > stream ? compute : stream);
-        return Choice{c, SplitPlan{(int)tile_count(p, c), 1, 0}, t};
+    switch (c) {
+    case F32_128x128_O3: return 1.0091;
+    case F32_128x64: return 0.9656;
+    case F32_64x128: return 0.9732;
+    case F32_64x64: return 0.9478;
+    case F32_256x128: return 1.0157;
+    case F64_64x64: return 0.9837;
+    default: return 1.0;
     }
+}
+
+// Large fp32 shapes (epi set): the part of a tile's epilogue the CU's other
+// workgroups do not hide, kEpiSec per byte of the C tile, times 12 for C rows
+// that take no vector access (single-element loads and stores), and per
+// split part kEpiSec per byte of its partial; both times 0.2 at three
+// workgroups per CU.
+constexpr double kEpiSec = 2.2496e-13;
+
+// The small-problem kernel (one launch of 32x32 tiles, w = 2*32*32*K flops
+// each): a workgroup alone on a CU computes at kSmallRate; past one
+// workgroup per CU the CU's kSmallCuRate limits; fp64 at kSmallF64Rate and
+// kSmallF64CuRate of those.  Each workgroup adds kSmallWgSec, the launch
+// kSmallSec, and its operand bytes over kSmallBw (kSmallBwBatch for a batch,
+// whose entries' slabs are contiguous) bound it from below.
+constexpr double kSmallRate = 3.0164e11;
+constexpr double kSmallCuRate = 3.4791e11;
+constexpr double kSmallF64Rate = 0.7701;
+constexpr double kSmallF64CuRate = 0.5625;
+constexpr double kSmallBw = 4.4151e12;
+constexpr double kSmallBwBatch = 7.0462e12;
+constexpr double kSmallSec = 3.955e-6;
+constexpr double kSmallWgSec = 5.184e-7;
+constexpr double kSmall8 = 1.0819;  // the 8-wave form, relative to the 4-wave one
+// Its waves read operands straight from memory in the MFMA lane layout, so a
+// k-contiguous operand is read as one 16-byte run per row per lane and
+// touches many more cache lines per load than an x-contiguous one; the
+// factors by which the compute terms grow with k-contiguous operands:
+constexpr double kSmallLayF32Both = 1.0565;  // fp32, A and B (A or B alone: 1)
+constexpr double kSmallLayF64Both = 1.0430;
+constexpr double kSmallLayF64A = 1.1539;
+constexpr double kSmallLayF64B = 1.1529;
+
+// The split-K space of a tile config: whole rounds run unsplit, and the
+// `rem` tiles of the tail (every tile of every entry, for a batch whose grid
+// fills less than one round) may be cut into 2 .. smax k-ranges of at least
+// two k tiles each.  smax == 0: no split (the small-problem and generic
+// kernels, fewer than four k tiles, a batch that fills a round, no tail).
+// Entry z's partials follow entry z-1's, so the workspace holds one launch's
+// entries (zmax).
+struct SplitSpace {
+    int64_t tiles, full, rem, smax, zmax, nb;
+    SplitPlan plan(int64_t split) const
+    {
+        if (split <= 1 || smax == 0) return SplitPlan{(int)tiles, 1, 0};
+        return SplitPlan{(int)full, (int)split, (int)rem};
+    }
+};
+
+SplitSpace split_space(const Problem& p, Cfg c, int64_t cus)
+{
+    const int64_t nb = p.batch > 1 ? p.batch : 1;
+    const int64_t tiles = tile_count(p, c);
+    SplitSpace s{tiles, tiles, 0, 0, nb < kMaxGridZ ? nb : kMaxGridZ, nb};
+    if (c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8 || c == GENERIC) return s;
     const CfgInfo& ci = kCfg[c];
-    const double rate = p.dtype == SBX_F32 ? 0.55e12 : 0.275e12;
-    const double F = 4e-6, G = 7.5e-6, W = 6e12;
-    const double e1 = 0.9;
+    const int64_t P = ci.per_cu;
+    const int64_t nk = cdiv(p.k, ci.bk);
+    if (nk < 4) return s;
+    if (nb > 1 && tiles * nb >= P * cus) return s;
+    const int64_t rem = nb > 1 ? tiles : tiles >= P * cus ? tiles % (P * cus) : tiles;
+    if (rem == 0) return s;
+    s.rem = rem;
+    s.full = tiles - rem;
+    s.smax = nk / 2 < kMaxSplit ? nk / 2 : kMaxSplit;
+    return s;
+}
+
+// Bytes of split partials a plan writes (one launch's entries).
+size_t split_bytes(const Problem& p, Cfg c, const SplitSpace& ss, int64_t split)
+{
+    const size_t elem = p.dtype == SBX_F32 ? 4 : 8;
+    return (size_t)(ss.rem * split * ss.zmax) * kCfg[c].bm * kCfg[c].bn * elem;
+}
+
+double small_seconds(const Problem& p, Cfg c, int64_t cus, const SplitSpace& ss)
+{
+    const bool f64 = c == F64_SMALL;
+    const bool akc = !p.ta, bkc = p.tb;
+    const double lay = f64 ? (akc && bkc ? kSmallLayF64Both : akc ? kSmallLayF64A
+                                                        : bkc ? kSmallLayF64B : 1.0)
+                           : (akc && bkc ? kSmallLayF32Both : 1.0);
+    const int64_t units = tile_count(p, c) * ss.nb;
+    const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
+    const double lat = (double)cdiv(units, 2 * cus) *
+                       (w / (kSmallRate * (f64 ? kSmallF64Rate : 1.0)) + kSmallWgSec);
+    const double thr = (double)cdiv(units, cus) *
+                       (w / (kSmallCuRate * (f64 ? kSmallF64CuRate : 1.0)) + kSmallWgSec);
+    const double elem = f64 ? 8.0 : 4.0;
+    const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
+                         (double)ss.nb;
+    const double stream = bytes / (p.batch > 1 ? kSmallBwBatch : kSmallBw);
+    const double compute = (lat > thr ? lat : thr) * lay;
+    const double t = kSmallSec + (compute > stream ? compute : stream);
+    return c == F32_SMALL8 ? t * kSmall8 : t;
+}
+
+// Modelled seconds of config c with `split` k-ranges of its tail (1: none).
+double plan_seconds(const Problem& p, Cfg c, int64_t cus, const SplitSpace& ss, int64_t split,
+                    bool epi)
+{
+    if (c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8) return small_seconds(p, c, cus, ss);
+    const CfgInfo& ci = kCfg[c];
+    const double rate = (p.dtype == SBX_F32 ? kRateF32 : kRateF64) * cfg_eff(c);
     const double elem = p.dtype == SBX_F32 ? 4.0 : 8.0;
     const int64_t P = ci.per_cu;
+    const double c_bytes = (double)ci.bm * ci.bn * elem;
     double o_tile = 0.0, o_part = 0.0;  // epilogue terms of a whole tile / a split part
     if (epi) {
         const int64_t vec_elems = 16 / (int64_t)elem;
         const bool vec = p.ldc % vec_elems == 0 && ((uintptr_t)p.C % 16) == 0;
         const double hide = P >= 3 ? 0.2 : 1.0;
-        const double c_bytes = (double)ci.bm * ci.bn * elem;
         o_tile = kEpiSec * c_bytes * hide * (vec ? 1.0 : 12.0);
         o_part = kEpiSec * c_bytes * hide;
     }
     const double wk = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // a whole tile's MFMA work
-    const double w = wk + o_tile;
+    const double w = wk + o_tile + kTileSec + c_bytes / kTileStoreBw;
+    if (split <= 1 || ss.smax == 0) return rounds_time(ss.tiles * ss.nb, w, P, cus, kE1) + kGridSec;
+    const int64_t sp = split;
+    return rounds_time(ss.full * ss.nb, w, P, cus, kE1) +
+           rounds_time(ss.rem * sp * ss.nb, wk / (double)sp + o_part + kPartSec, P, cus, kE1) +
+           kGridSec + kReduceSec + (double)(ss.rem * sp * ss.nb) * c_bytes / kReduceBw;
+}
 
-    const int64_t tiles = tile_count(p, c);
-    const int64_t units = tiles * (p.batch > 1 ? p.batch : 1);
-    Choice best{c, SplitPlan{(int)tiles, 1, 0}, rounds_time(units, w, P, cus, e1) + F};
-    const int64_t nk = cdiv(p.k, ci.bk);
-    if (nk < 4) return best;
-    // A batch splits every tile of every entry, and only where its grid
-    // fills less than one round of the chip (128 x 128^2 x 1024 on 128^2
-    // tiles: 128 workgroups for 512 slots).  Entry z's partials follow
-    // entry z-1's, so the workspace holds one launch's entries.
-    const int64_t nb = p.batch > 1 ? p.batch : 1;
-    const int64_t zmax = nb < kMaxGridZ ? nb : kMaxGridZ;
-    if (nb > 1 && units >= P * cus) return best;
-    const int64_t rem = nb > 1 ? tiles : tiles >= P * cus ? tiles % (P * cus) : tiles;
-    if (rem == 0) return best;
-    const int64_t full = tiles - rem;
-    const int64_t smax = nk / 2 < kMaxSplit ? nk / 2 : kMaxSplit;
-    for (int64_t sp = 2; sp <= smax; ++sp) {
-        if ((size_t)(rem * sp * zmax) * ci.bm * ci.bn * (size_t)elem > max_ws) break;
-        const double t = rounds_time(full * nb, w, P, cus, e1) +
-                         rounds_time(rem * sp * nb, wk / (double)sp + o_part + kPartSec, P, cus, e1) +
-                         F + G + (double)(rem * sp * nb) * ci.bm * ci.bn * elem / W;
-        if (t < best.seconds * 0.98)
-            best = Choice{c, SplitPlan{(int)full, (int)sp, (int)rem}, t};
+// The split counts a plan may use (beyond 1, unsplit): every count to 8, then
+// coarser steps, so that a pick is one of the plans that were timed.
+constexpr int kSplitSet[] = {2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 28, 32};
+static_assert(kMaxSplit == 32, "kSplitSet ends at kMaxSplit");
+
+// The model's plan for config c: unsplit, or the split predicted >= 0.5 %
+// faster than every smaller one (a split's partials cost memory; at 2 % the
+// fp64 8192^2 x 8192 SYRK stopped at 4 parts, 7514 us, where 8-24 parts
+// took 7367-7374 us).  max_ws: the most split-partial bytes a plan may use
+// (the allocation-free entry point's scratch size; unlimited otherwise).
+Choice model_plan(const Problem& p, Cfg c, int64_t cus, size_t max_ws, bool epi = false)
+{
+    const SplitSpace ss = split_space(p, c, cus);
+    Choice best{c, ss.plan(1), plan_seconds(p, c, cus, ss, 1, epi)};
+    for (int sp : kSplitSet) {
+        if (sp > ss.smax || split_bytes(p, c, ss, sp) > max_ws) break;
+        const double t = plan_seconds(p, c, cus, ss, sp, epi);
+        if (t < best.seconds * 0.995) best = Choice{c, ss.plan(sp), t};
     }
     return best;
 }
@@ -642,16 +696,77 @@ struct FixedScratch {
     std::mutex* launch_mu;
 };
 
+// A plan the caller names (sbx_gemm_ex_plan): a tile config and the number
+// of k-ranges its tail is cut into (1: unsplit).
+struct ForcedPlan {
+    Cfg cfg;
+    int split;
+};
+
+// Element type a config computes in; -1 for the generic kernel (both).
+int cfg_dtype(Cfg c)
+{
+    if (c == GENERIC) return -1;
+    return strstr(kCfg[c].name, "_f64_") ? SBX_F64 : SBX_F32;
+}
+
+// "<config name>" or "<config name>+splitk<s>": the names sbx_gemm_select
+// reports and sbx_gemm_ex_plan accepts.
+void plan_name(Cfg c, int split, char* name, size_t cap)
+{
+    if (split > 1)
+        snprintf(name, cap, "%s+splitk%d", kCfg[c].name, split);
+    else
+        snprintf(name, cap, "%s", kCfg[c].name);
+}
+
+bool parse_plan(const char* name, ForcedPlan* out)
+{
+    if (!name) return false;
+    const char* plus = strstr(name, "+splitk");
+    const size_t len = plus ? (size_t)(plus - name) : strlen(name);
+    int split = 1;
+    if (plus) {
+        char* end = nullptr;
+        const long v = strtol(plus + 7, &end, 10);
+        if (end == plus + 7 || *end != '\0' || v < 2 || v > kMaxSplit) return false;
+        split = (int)v;
+    }
+    for (int c = 0; c <= GENERIC; ++c)
+        if (strlen(kCfg[c].name) == len && strncmp(kCfg[c].name, name, len) == 0) {
+            *out = ForcedPlan{(Cfg)c, split};
+            return true;
+        }
+    return false;
+}
+
 // fixed: the caller's split workspace; null: the stream's cached one.
+// forced: run this plan instead of the model's (SBX_UNSUPPORTED if the
+// problem cannot use it).
 template <typename T>
 int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* chosen,
-        SplitPlan* chosen_split, const FixedScratch* fixed = nullptr)
+        SplitPlan* chosen_split, const FixedScratch* fixed = nullptr,
+        const ForcedPlan* forced = nullptr)
 {
     if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
     const bool quick = alpha == (T)0 || p.k == 0;
     Cfg cfg = GENERIC;
     SplitPlan sp{0, 1, 0};
-    if (algo != SBX_ALGO_GENERIC) {
+    if (forced) {
+        const int dt = cfg_dtype(forced->cfg);
+        if ((dt >= 0 && dt != p.dtype) || p.table) return SBX_UNSUPPORTED;
+        // a triangle takes only the square tile configs its candidates list
+        if (p.uplo && forced->cfg != F32_256x256 && forced->cfg != F32_128x128 &&
+            forced->cfg != F32_128x128_O3 && forced->cfg != F64_128x128)
+            return SBX_UNSUPPORTED;
+        const bool tile = forced->cfg != GENERIC && forced->cfg != F32_SMALL &&
+                          forced->cfg != F64_SMALL && forced->cfg != F32_SMALL8;
+        if (tile && !mfma_feasible(p, forced->cfg)) return SBX_UNSUPPORTED;
+        const SplitSpace ss = split_space(p, forced->cfg, cu_count());
+        if (forced->split > 1 && forced->split > ss.smax) return SBX_UNSUPPORTED;
+        cfg = forced->cfg;
+        sp = ss.plan(forced->split);
+    } else if (algo != SBX_ALGO_GENERIC) {
         Cfg cands[kMaxCands];
         const int64_t cus = cu_count();
         // no workspace for hipStreamPerThread: plan unsplit
@@ -662,49 +777,12 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
         for (int i = 0; i < nc; ++i) {
             if (!mfma_feasible(p, cands[i])) continue;
-            const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL;
+            const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL ||
+                               cands[i] == F32_SMALL8;
             if (algo == SBX_ALGO_MFMA_TILE && small) continue;
             if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
             const Choice c = model_plan(p, cands[i], cus, max_ws, large);
-            // The 8-wave 256x64 tile off whole rounds only with a split
-            // tail: unsplit, its last partial round ran behind 128x64 at
-            // two per CU (100000x63x515: 86 against 82 us), which the
-            // model rates alike; with a split tail it won (80000x64x2048
-            // +splitk4: 195 against 210 us unsplit 128x64).  Its 64x256
-            // mirror only on whole rounds: off them the 64x128 tile with a
-            // split tail was 2-4 % faster than it, split or not
-            // (48x100000x1024, 64x70000x2048, 64x80000x2048).
-            const int64_t units = tile_count(p, cands[i]) * (p.batch > 1 ? p.batch : 1);
-            const bool whole = units % cus == 0;
-            // The fp32 64^2 tile only up to two rounds (at two per CU): over
-            // more it ran 4-5 % behind the larger tiles, which the model
-            // rates alike (2048^3: 127 against 121 us for 64x128; 3000^3
-            // +splitk3: 415 against 394 us for 128^2 +splitk4).
-            if (cands[i] == F32_64x64 && units > 4 * cus) continue;
-            // Nor for a batch whose entries the 64x128 tile covers exactly:
-            // its larger wave tile wins although the model rates the 64^2
-            // grid's finer rounds ahead (128 x 128^2 x 1024: 35.4 against
-            // 42.1 us, 64 x 128^2 x 2048: 43.9 against 55.0); where both
-            // pad (16 x 200^2 x 2000: 36.5 against 40.2 us) or only 64x128
-            // does (32 x 192^2 x 1536 +splitk3: 46.1 against 59.1), 64^2
-            // stays ahead, as it does split (8 x 128^2 x 4096 +splitk8:
-            // 16.2 us).
-            if (cands[i] == F32_64x64 && p.batch > 1 && c.sp.split == 1 && p.m % 64 == 0 &&
-                p.n % 128 == 0)
-                continue;
-            // fp64 likewise, where the 64x128 grid fills one to two workgroups
-            // per CU unsplit (128 x 128^2 x 1024: 70.9 against 106.0 us, 64 x
-            // 256^3: 38.5 against 41.5); with fewer it splits and with more
-            // its part round trails, and 64^2 led (16 x 256^2 x 2048: 67.8
-            // against 73.0 us, 32 x 384^3: 68.8 against 74.6).
-            if (cands[i] == F64_64x64 && p.batch > 1 && c.sp.split == 1 && p.m % 64 == 0 &&
-                p.n % 128 == 0) {
-                const int64_t wu = tile_count(p, F64_64x128) * p.batch;
-                if (wu >= cus && wu <= 2 * cus) continue;
-            }
-            if (cands[i] == F32_256x64 && c.sp.split == 1 && !whole) continue;
-            if (cands[i] == F32_64x256 && !whole) continue;
-            if (!any || c.seconds < best.seconds * 0.97) best = c;  // first candidate is the default
+            if (!any || c.seconds < best.seconds) best = c;  // ties keep the earlier candidate
             any = true;
         }
         if (!any && algo != SBX_ALGO_AUTO) return SBX_UNSUPPORTED;
@@ -712,13 +790,6 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             cfg = best.cfg;
             sp = best.sp;
         }
-        // With at most one 32x32 tile per CU and a long K, cutting K over 8
-        // waves shortens each wave's chain of dependent loads (512^3: 6.45 ->
-        // 6.19 us, 256^2 x 4096: 37.6 -> 29.2 us); with more tiles per CU the
-        // 4-wave form keeps more workgroups resident and wins.
-        if (cfg == F32_SMALL && p.k >= 512 &&
-            tile_count(p, cfg) * (p.batch > 1 ? p.batch : 1) <= cus)
-            cfg = F32_SMALL8;
     }
     const CfgInfo& info = kCfg[cfg];
     const int64_t tiles = tile_count(p, cfg);
@@ -798,7 +869,8 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
               int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
               int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
               void* C, int64_t ldc, int64_t str_c, int64_t batch, int algo, int epilogue,
-              Cfg* chosen, SplitPlan* chosen_split, const FixedScratch* fixed = nullptr)
+              Cfg* chosen, SplitPlan* chosen_split, const FixedScratch* fixed = nullptr,
+              const ForcedPlan* forced = nullptr, Problem* problem = nullptr)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (epilogue != SBX_EPILOGUE_NONE && epilogue != SBX_EPILOGUE_RELU) return SBX_INVALID_ARGUMENT;
@@ -842,13 +914,17 @@ int gemm_impl(void* stream, int dtype, int layout, int transA, int transB, int64
     p.table = nullptr;
     p.table_swap = 0;
     if (batch <= 1) { p.str_a = 0; p.str_b = 0; }
+    if (problem) {  // the validated problem only (plan enumeration)
+        *problem = p;
+        return SBX_OK;
+    }
 
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, algo, s, chosen,
-                          chosen_split, fixed);
+                          chosen_split, fixed, forced);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, algo, s, chosen,
-                       chosen_split, fixed);
+                       chosen_split, fixed, forced);
 }
 
 // Grouped GEMM: `count` problems of one shape and one set of scalars whose
@@ -899,6 +975,40 @@ int grouped_impl(void* stream, int dtype, int layout, int transA, int transB, in
                        nullptr);
 }
 
+// One line "<plan name> <predicted microseconds>" per plan the heuristics
+// weigh for problem p (every candidate config, unsplit and at each split of
+// kSplitSet its split space allows), the pick among them.
+int write_plans(const Problem& p, char* out, size_t cap)
+{
+    out[0] = '\0';
+    if (p.m == 0 || p.n == 0 || p.batch == 0) return SBX_OK;
+    const int64_t cus = cu_count();
+    Cfg cands[kMaxCands];
+    bool large = false;
+    const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
+    size_t used = 0;
+    for (int i = 0; i < nc; ++i) {
+        const Cfg c = cands[i];
+        const bool small = c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8;
+        if (!small && !mfma_feasible(p, c)) continue;
+        const SplitSpace ss = split_space(p, c, cus);
+        for (int j = -1; j < (int)(sizeof(kSplitSet) / sizeof(int)); ++j) {
+            const int s = j < 0 ? 1 : kSplitSet[j];
+            if (s > 1 && s > ss.smax) break;
+            char name[96];
+            plan_name(c, s, name, sizeof(name));
+            const double us = plan_seconds(p, c, cus, ss, s, large) * 1e6;
+            const int w = snprintf(out + used, cap - used, "%s %.3f\n", name, us);
+            if (w < 0 || (size_t)w >= cap - used) {
+                out[used] = '\0';
+                return SBX_INVALID_ARGUMENT;  // buffer too small
+            }
+            used += (size_t)w;
+        }
+    }
+    return SBX_OK;
+}
+
 // SYRK: C = alpha * op(A) op(A)^T + beta * C on one triangle of the n x n C
 // (the arithmetic of oneMKL's syrk / syrk_batch, syrk.cpp:44-77), run as a
 // GEMM with B = A whose tile grid covers only that triangle.  Row-major:
@@ -909,7 +1019,8 @@ int grouped_impl(void* stream, int dtype, int layout, int transA, int transB, in
 int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
               const void* alpha, const void* A, int64_t lda, int64_t str_a, const void* beta,
               void* C, int64_t ldc, int64_t str_c, int64_t batch, Cfg* chosen = nullptr,
-              SplitPlan* chosen_split = nullptr)
+              SplitPlan* chosen_split = nullptr, const ForcedPlan* forced = nullptr,
+              Problem* problem = nullptr)
 {
     if (dtype != SBX_F32 && dtype != SBX_F64) return SBX_UNSUPPORTED;
     if (layout != 0 && layout != 1) return SBX_INVALID_ARGUMENT;
@@ -942,12 +1053,16 @@ int syrk_impl(void* stream, int dtype, int layout, int upper, int trans, int64_t
     p.uplo = up ? 2 : 1;
     p.table = nullptr;
     p.table_swap = 0;
+    if (problem) {
+        *problem = p;
+        return SBX_OK;
+    }
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SBX_F32)
         return run<float>(p, *(const float*)alpha, *(const float*)beta, SBX_ALGO_AUTO, s,
-                          chosen, chosen_split);
+                          chosen, chosen_split, nullptr, forced);
     return run<double>(p, *(const double*)alpha, *(const double*)beta, SBX_ALGO_AUTO, s,
-                       chosen, chosen_split);
+                       chosen, chosen_split, nullptr, forced);
 }
 
 // GEMV: y = alpha * op(A) x + beta * y (oneMKL gemv, gemv.cpp:44-61), netlib
@@ -1231,11 +1346,43 @@ int sbx_gemm_select_batched(int dtype, int layout, int transA, int transB, int64
                             str_a, fake, ldb, str_b, one, (void*)fake, ldc, str_c, batch,
                             SBX_ALGO_AUTO, SBX_EPILOGUE_NONE, &cfg, &sp);
     if (st != SBX_OK) return st;
-    if (sp.split > 1)
-        snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);
-    else
-        snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
+    sbx::plan_name(cfg, sp.split, name, cap);
     return SBX_OK;
+}
+
+int sbx_gemm_plans(int dtype, int layout, int transA, int transB, int64_t m, int64_t n,
+                   int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch, char* out,
+                   size_t cap)
+{
+    if (!out || cap == 0) return SBX_INVALID_ARGUMENT;
+    if (batch < 1) return SBX_INVALID_ARGUMENT;
+    const int64_t rows_a = (layout == 0) == !transA ? m : k;
+    const int64_t rows_b = (layout == 0) == !transB ? k : n;
+    const int64_t rows_c = layout == 0 ? m : n;
+    static const float one_f = 1.0f;
+    static const double one_d = 1.0;
+    const void* one = dtype == SBX_F64 ? (const void*)&one_d : (const void*)&one_f;
+    const void* fake = (const void*)(uintptr_t)0x1000;
+    sbx::Problem p;
+    int st = sbx::gemm_impl((void*)-1, dtype, layout, transA, transB, m, n, k, one, fake, lda,
+                            rows_a * lda, fake, ldb, rows_b * ldb, one, (void*)fake, ldc,
+                            rows_c * ldc, batch, SBX_ALGO_AUTO, SBX_EPILOGUE_NONE, nullptr,
+                            nullptr, nullptr, nullptr, &p);
+    if (st != SBX_OK) return st;
+    return sbx::write_plans(p, out, cap);
+}
+
+int sbx_gemm_ex_plan(void* stream, int dtype, int layout, int transA, int transB, int64_t m,
+                     int64_t n, int64_t k, const void* alpha, const void* A, int64_t lda,
+                     int64_t str_a, const void* B, int64_t ldb, int64_t str_b, const void* beta,
+                     void* C, int64_t ldc, int64_t str_c, int64_t batch, const char* plan)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    sbx::ForcedPlan fp;
+    if (!sbx::parse_plan(plan, &fp)) return SBX_INVALID_ARGUMENT;
+    return sbx::gemm_impl(stream, dtype, layout, transA, transB, m, n, k, alpha, A, lda, str_a,
+                          B, ldb, str_b, beta, C, ldc, str_c, batch, SBX_ALGO_AUTO,
+                          SBX_EPILOGUE_NONE, nullptr, nullptr, nullptr, &fp);
 }
 
 int sbx_syrk_select(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
@@ -1251,11 +1398,35 @@ int sbx_syrk_select(int dtype, int layout, int upper, int trans, int64_t n, int6
     int st = sbx::syrk_impl((void*)-1, dtype, layout, upper, trans, n, k, one, fake, lda, 0, one,
                             (void*)fake, ldc, 0, 1, &cfg, &sp);
     if (st != SBX_OK) return st;
-    if (sp.split > 1)
-        snprintf(name, cap, "%s+splitk%d", sbx::kCfg[cfg].name, sp.split);
-    else
-        snprintf(name, cap, "%s", sbx::kCfg[cfg].name);
+    sbx::plan_name(cfg, sp.split, name, cap);
     return SBX_OK;
+}
+
+int sbx_syrk_plans(int dtype, int layout, int upper, int trans, int64_t n, int64_t k,
+                   int64_t lda, int64_t ldc, char* out, size_t cap)
+{
+    if (!out || cap == 0) return SBX_INVALID_ARGUMENT;
+    static const float one_f = 1.0f;
+    static const double one_d = 1.0;
+    const void* one = dtype == SBX_F64 ? (const void*)&one_d : (const void*)&one_f;
+    const void* fake = (const void*)(uintptr_t)0x1000;
+    sbx::Problem p;
+    const int st = sbx::syrk_impl((void*)-1, dtype, layout, upper, trans, n, k, one, fake, lda, 0,
+                                  one, (void*)fake, ldc, 0, 1, nullptr, nullptr, nullptr, &p);
+    if (st != SBX_OK) return st;
+    return sbx::write_plans(p, out, cap);
+}
+
+int sbx_syrk_ex_plan(void* stream, int dtype, int layout, int upper, int trans, int64_t n,
+                     int64_t k, const void* alpha, const void* A, int64_t lda, int64_t str_a,
+                     const void* beta, void* C, int64_t ldc, int64_t str_c, int64_t batch,
+                     const char* plan)
+{
+    if (stream == (void*)-1) return SBX_INVALID_ARGUMENT;
+    sbx::ForcedPlan fp;
+    if (!sbx::parse_plan(plan, &fp)) return SBX_INVALID_ARGUMENT;
+    return sbx::syrk_impl(stream, dtype, layout, upper, trans, n, k, alpha, A, lda, str_a, beta, C,
+                          ldc, str_c, batch, nullptr, nullptr, &fp);
 }
 
 const char* sbx_status_string(int status)

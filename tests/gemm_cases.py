@@ -58,9 +58,10 @@ def c_window(layout, C, m, n, ldc):
 
 
 def run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-            algo=0, offsets=(0, 0, 0), epilogue=None):
-    """Copy host buffers to the GPU, run sbx_gemm_ex (or sbx_gemm_fused when
-    `epilogue` is given), return the new host C.
+            algo=0, offsets=(0, 0, 0), epilogue=None, plan=None):
+    """Copy host buffers to the GPU, run sbx_gemm_ex (sbx_gemm_fused when
+    `epilogue` is given, sbx_gemm_ex_plan with the named plan when `plan`
+    is), return the new host C.
 
     `offsets` shifts each device buffer by that many elements (to exercise
     pointers that are not 16-byte aligned)."""
@@ -77,7 +78,10 @@ def run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C,
     ptrs = (dA.data_ptr() + es * offsets[0], dB.data_ptr() + es * offsets[1],
             dC.data_ptr() + es * offsets[2])
     code = sbx.F32 if dtype == np.float32 else sbx.F64
-    if epilogue is None:
+    if plan is not None:
+        sbx.gemm_ex_plan(code, layout, ta, tb, m, n, k, alpha, ptrs[0], lda, 0, ptrs[1], ldb, 0,
+                         beta, ptrs[2], ldc, 0, 1, plan)
+    elif epilogue is None:
         sbx.gemm_ex(code, layout, ta, tb, m, n, k, alpha, ptrs[0], lda, 0, ptrs[1], ldb, 0,
                     beta, ptrs[2], ldc, 0, 1, algo)
     else:

@@ -19,10 +19,10 @@ SEED = 20261201
 
 
 def _case(dev, dtype, layout, ta, tb, m, n, k, alpha, beta, seed, algo=0, pad=(0, 0, 0),
-          offsets=(0, 0, 0), dist="uniform"):
+          offsets=(0, 0, 0), dist="uniform", plan=None):
     A, lda, B, ldb, C, ldc = make_inputs(dtype, layout, ta, tb, m, n, k, seed, pad, dist)
     got = run_sbx(dev, dtype, layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-                  algo, offsets)
+                  algo, offsets, plan=plan)
     want = run_oracle(layout, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
     err = normwise(layout, got, want, m, n, ldc)
     print(f"case dtype={np.dtype(dtype).name} layout={layout} tA={ta} tB={tb} "
@@ -402,40 +402,32 @@ def test_deep_forward_pass_closed_form(cuda):
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
-    """The 128x128 fp32 tile compiled for three workgroups per CU: 768 ragged
-    tiles in one round (scalar loads, odd ld) and, at 3584^2 x 512, a full
-    round plus a tail split six ways."""
-    import sushiblas_amd as sbx
-    for i, (m, n, k, beta) in enumerate([(4095, 3001, 96, 1.0), (3584, 3584, 512, 0.5)]):
-        sa = (k, m) if ta else (m, k)
-        sbd = (n, k) if tb else (k, n)
-        lda = sa[1] if layout == 0 else sa[0]
-        ldb = sbd[1] if layout == 0 else sbd[0]
-        ldc = n if layout == 0 else m
-        name = sbx.gemm_select(sbx.F32, layout, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"three-per-CU case {m}x{n}x{k} -> {name}", flush=True)
-        if i == 1:
-            assert name == "mfma_f32_128x128x16_w2x2_o3+splitk6", name
-        err, _, _ = _case(cuda, np.float32, layout, ta, tb, m, n, k, 1.0, beta, SEED + 60 + i)
-        assert err <= TOL[np.float32], (m, n, k, name)
+    """The 128x128 fp32 tile compiled for three workgroups per CU (run by
+    name, sbx_gemm_ex_plan): 768 ragged tiles in one round (scalar loads, odd
+    ld) and, at 3584^2 x 512, a full round plus a tail split six ways."""
+    for i, (m, n, k, beta, plan) in enumerate([
+            (4095, 3001, 96, 1.0, "mfma_f32_128x128x16_w2x2_o3"),
+            (3584, 3584, 512, 0.5, "mfma_f32_128x128x16_w2x2_o3+splitk6")]):
+        print(f"three-per-CU case {m}x{n}x{k} -> {plan}", flush=True)
+        err, _, _ = _case(cuda, np.float32, layout, ta, tb, m, n, k, 1.0, beta, SEED + 60 + i,
+                          plan=plan)
+        assert err <= TOL[np.float32], (m, n, k, plan)
 
 
 # -- the small-problem kernel with K cut over 8 waves ---------------------------
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_small_kernel_eight_waves(cuda, ta, tb):
-    """At most one 32x32 tile per CU and K >= 512 select the 8-wave form:
-    512^3, and a ragged 300 x 200 x 1001 with padded leading dimensions and
-    misaligned bases (K tail, partial tiles); C outside the window untouched."""
-    import sushiblas_amd as sbx
+    """The small-problem kernel's 8-wave form, run by name: 512^3, and a
+    ragged 300 x 200 x 1001 with padded leading dimensions and misaligned
+    bases (K tail, partial tiles); C outside the window untouched."""
+    plan = "mfma_f32_32x32_ksplit8"
     for i, (m, n, k, pad, off) in enumerate([(512, 512, 512, (0, 0, 0), (0, 0, 0)),
                                              (300, 200, 1001, (3, 1, 5), (1, 2, 3))]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i, pad)
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"eight-wave case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == "mfma_f32_32x32_ksplit8", name
+        print(f"eight-wave case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
         got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc,
-                      offsets=off)
+                      offsets=off, plan=plan)
         want = run_oracle(0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -450,19 +442,17 @@ def test_large_tiles_ragged_edges(cuda, ta, tb):
     tail (257 = 16*16 + 1) and padded leading dimensions.  With ldc = n + 5
     no C row allows vector access, and the same shape runs the three-per-CU
     128^2 tile, whose interior tiles then load and store C one element at a
-    time.  4097 x 8191 x 515 runs the 128x128 tile with a split tail.  The
-    ldc padding of C stays untouched."""
-    import sushiblas_amd as sbx
+    time.  4097 x 8191 x 515 runs the 128x128 tile with a split tail.  Each
+    runs by name; the ldc padding of C stays untouched."""
     for i, (m, n, k, c_pad, want_name) in enumerate([
             (8191, 8190, 257, 6, "mfma_f32_256x128x16_w4x1"),
             (8191, 8190, 257, 5, "mfma_f32_128x128x16_w2x2_o3"),
             (4097, 8191, 515, 5, "mfma_f32_128x128x16_w2x2+splitk4")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 80 + i,
                                              pad=(3, 1, c_pad))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"large-tile case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == want_name, name
-        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        print(f"large-tile case {m}x{n}x{k} t{ta}{tb} -> {want_name}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc,
+                      plan=want_name)
         want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -473,16 +463,15 @@ def test_large_tiles_ragged_edges(cuda, ta, tb):
 def test_tall_skinny_eight_wave_tile(cuda, ta, tb):
     """The 8-wave 256x64 tile (n <= 64 with a full round of 256-row tiles):
     a ragged last row tile, n = 63, a K tail (515 = 16*32 + 3) and padded
-    leading dimensions; 65536 x 64 x 1000 is a whole round with a K tail.  The
-    ldc padding of C stays untouched."""
-    import sushiblas_amd as sbx
+    leading dimensions; 65536 x 64 x 1000 is a whole round with a K tail.  Run
+    by name; the ldc padding of C stays untouched."""
+    plan = "mfma_f32_256x64x32_w8x1"
     for i, (m, n, k) in enumerate([(65535, 63, 515), (65536, 64, 1000)]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name.startswith("mfma_f32_256x64x32_w8x1"), name
-        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc,
+                      plan=plan)
         want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -494,16 +483,15 @@ def test_wide_eight_wave_tile(cuda, ta, tb):
     """The 8-wave 64x256 tile, the tall tile's mirror (m <= 64 with a full
     round of 256-column tiles): a ragged last column tile, m = 63 and a K
     tail (515); 64 x 65536 x 1100, whose B (288 MB) is loaded
-    non-temporal; m = 48.  Padded leading dimensions; the ldc padding of C
-    stays untouched."""
-    import sushiblas_amd as sbx
+    non-temporal; m = 48.  Run by name; padded leading dimensions; the ldc
+    padding of C stays untouched."""
+    plan = "mfma_f32_64x256x32_w1x8"
     for i, (m, n, k) in enumerate([(63, 65535, 515), (64, 65536, 1100), (48, 65536, 2048)]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 84 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"wide case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == "mfma_f32_64x256x32_w1x8", name
-        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        print(f"wide case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc,
+                      plan=plan)
         want = run_oracle(0, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -515,8 +503,8 @@ def test_narrow_tiles(cuda, ta, tb):
     """The 32-wide tiles (128x32 for n <= 32, its 32x128 mirror for m <= 32):
     ragged last tiles with a K tail (515); a split tail (40000 x 32 x 2048,
     3 parts); an operand above 256 MiB loaded non-temporal (1100 deep);
-    n = 1.  Padded leading dimensions; the ldc padding of C stays untouched."""
-    import sushiblas_amd as sbx
+    n = 1.  Run by name; padded leading dimensions; the ldc padding of C
+    stays untouched."""
     cases = [(65535, 31, 515, "mfma_f32_128x32x32_w4x1"),
              (40000, 32, 2048, "mfma_f32_128x32x32_w4x1+splitk3"),
              (65536, 32, 1100, "mfma_f32_128x32x32_w4x1"),
@@ -526,10 +514,9 @@ def test_narrow_tiles(cuda, ta, tb):
     for i, (m, n, k, want_name) in enumerate(cases):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 100 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"narrow case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == want_name, name
-        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.5, A, lda, B, ldb, 1.5, C, ldc)
+        print(f"narrow case {m}x{n}x{k} t{ta}{tb} -> {want_name}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.5, A, lda, B, ldb, 1.5, C, ldc,
+                      plan=want_name)
         want = run_oracle(0, ta, tb, m, n, k, -0.5, A, lda, B, ldb, 1.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -540,20 +527,17 @@ def test_narrow_tiles(cuda, ta, tb):
 def test_fp32_64x64_tile(cuda, ta, tb):
     """The fp32 64x64 tile (four waves of 32x32 on 32x32x2 MFMAs): ragged
     edges with K = 1023 (a k-contiguous vector straddles K) and with
-    misaligned bases; a split tail (1536 x 1536 x 1024, 4 parts).  Padded
-    leading dimensions; the ldc padding of C stays untouched."""
-    import sushiblas_amd as sbx
+    misaligned bases; a split tail (1536 x 1536 x 1024, 4 parts).  Run by
+    name; padded leading dimensions; the ldc padding of C stays untouched."""
     for i, (m, n, k, off, want_name) in enumerate([
             (1000, 1100, 1023, (0, 0, 0), "mfma_f32_64x64x32_w2x2"),
             (999, 1001, 1025, (1, 2, 3), "mfma_f32_64x64x32_w2x2"),
             (1536, 1536, 1024, (0, 0, 0), "mfma_f32_64x64x32_w2x2+splitk4")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 115 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"fp32 64x64 case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == want_name, name
+        print(f"fp32 64x64 case {m}x{n}x{k} t{ta}{tb} -> {want_name}", flush=True)
         got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.25, C, ldc,
-                      offsets=off)
+                      offsets=off, plan=want_name)
         want = run_oracle(0, ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.25, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -565,19 +549,17 @@ def test_fp64_64x64_tile(cuda, ta, tb):
     """The fp64 64x64 tile (four waves of 32x32, 16x16x4 fp64 MFMAs): ragged
     edges with an odd K (a k-contiguous vector straddles K); a split tail
     (1536^3, 4 parts); one tile cut 31 ways along a long K, whole and ragged
-    (m, n <= 64).  Padded leading dimensions; the ldc padding of C stays
-    untouched.  Bar 1e-12."""
-    import sushiblas_amd as sbx
+    (m, n <= 64).  Run by name; padded leading dimensions; the ldc padding
+    of C stays untouched.  Bar 1e-12."""
     for i, (m, n, k, want_name) in enumerate([(1500, 1300, 1023, "mfma_f64_64x64x16_w2x2"),
                                               (1536, 1536, 1536, "mfma_f64_64x64x16_w2x2+splitk4"),
                                               (64, 64, 8192, "mfma_f64_64x64x16_w2x2+splitk31"),
                                               (40, 17, 4099, "mfma_f64_64x64x16_w2x2+splitk31")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float64, 0, ta, tb, m, n, k, SEED + 110 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F64, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"fp64 64x64 case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == want_name, name
-        got = run_sbx(cuda, np.float64, 0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -1.25, C, ldc)
+        print(f"fp64 64x64 case {m}x{n}x{k} t{ta}{tb} -> {want_name}", flush=True)
+        got = run_sbx(cuda, np.float64, 0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -1.25, C, ldc,
+                      plan=want_name)
         want = run_oracle(0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -1.25, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float64], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -624,8 +606,8 @@ def test_split_k_strided_batch(cuda, dtype, layout, ta, tb, batch, m, n, k, want
     """A batch whose grid fills less than one round cuts K: every entry's
     tiles are split, entry z's partials after entry z-1's in the workspace,
     and the reduction finishes each entry's C (alpha, beta) in part order.
-    Each entry against the oracle, and the padding between entries of C
-    untouched.  Bars 1e-5 / 1e-12."""
+    Run by name.  Each entry against the oracle, and the padding between
+    entries of C untouched.  Bars 1e-5 / 1e-12."""
     import torch
     import sushiblas_amd as sbx
     code = sbx.F32 if dtype == np.float32 else sbx.F64
@@ -634,15 +616,14 @@ def test_split_k_strided_batch(cuda, dtype, layout, ta, tb, batch, m, n, k, want
     lda = sa[1] if layout == 0 else sa[0]
     ldb = sb[1] if layout == 0 else sb[0]
     ldc = n if layout == 0 else m
-    assert sbx.gemm_select(code, layout, ta, tb, m, n, k, lda, ldb, ldc, batch=batch) == want
     str_a, str_b, str_c = sa[0] * sa[1], sb[0] * sb[1], m * n + 4
     A = oracle.fill_uniform(batch * str_a, dtype, SEED + 130, 0)
     B = oracle.fill_uniform(batch * str_b, dtype, SEED + 130, 1)
     C = oracle.fill_uniform(batch * str_c, dtype, SEED + 130, 2)
     print(f"split batch {batch} x {m}x{n}x{k} layout={layout} t{ta}{tb} -> {want}", flush=True)
     dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
-    sbx.gemm_ex(code, layout, ta, tb, m, n, k, 0.75, dA, lda, str_a, dB, ldb, str_b, -0.5, dC,
-                ldc, str_c, batch)
+    sbx.gemm_ex_plan(code, layout, ta, tb, m, n, k, 0.75, dA, lda, str_a, dB, ldb, str_b, -0.5,
+                     dC, ldc, str_c, batch, want)
     torch.cuda.synchronize()
     got = dC.cpu().numpy()
     want_c = C.copy()
@@ -658,12 +639,11 @@ def test_split_k_strided_batch(cuda, dtype, layout, ta, tb, batch, m, n, k, want
 
 def test_column_major_tall_skinny(cuda):
     """cfg4's shape (65536 x 64 x 4096) in column-major storage: C^T = B^T A^T
-    makes it the wide row-major problem 64 x 65536 x 4096, which runs on the
-    64x256 tile with the long operand loaded non-temporal."""
-    import sushiblas_amd as sbx
+    makes it the wide row-major problem 64 x 65536 x 4096, run on the 64x256
+    tile (its pick) with the long operand loaded non-temporal."""
     m, n, k = 65536, 64, 4096
-    assert sbx.gemm_select(sbx.F32, 1, 0, 0, m, n, k, m, k, m) == "mfma_f32_64x256x32_w1x8"
-    err, _, _ = _case(cuda, np.float32, 1, 0, 0, m, n, k, 1.0, 0.0, SEED + 87)
+    err, _, _ = _case(cuda, np.float32, 1, 0, 0, m, n, k, 1.0, 0.0, SEED + 87,
+                      plan="mfma_f32_64x256x32_w1x8")
     assert err <= TOL[np.float32]
 
 
@@ -673,20 +653,18 @@ def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
     80000 x 64 x 2048 runs 256 whole tiles plus a 57-tile tail cut 4 ways
     (its split partials fill 16384-element workspace slots and the reduction
     walks 64 chunks of each), and 131000 x 63 x 515 runs two whole rounds
-    of 256 tiles (a ragged last row tile, n = 63 and a K tail).  Unsplit
-    with a partial last round, 100000 x 63 x 515 goes to the 128x64 tile.
-    Padded leading dimensions; the ldc padding of C stays untouched."""
-    import sushiblas_amd as sbx
+    of 256 tiles (a ragged last row tile, n = 63 and a K tail); 100000 x 63
+    x 515 on the 128x64 tile, unsplit with a partial last round.  Run by
+    name; padded leading dimensions; the ldc padding of C stays untouched."""
     for i, (m, n, k, want_name) in enumerate([
             (80000, 64, 2048, "mfma_f32_256x64x32_w8x1+splitk4"),
             (131000, 63, 515, "mfma_f32_256x64x32_w8x1"),
             (100000, 63, 515, "mfma_f32_128x64x32_w2x2")]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 96 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(sbx.F32, 0, ta, tb, m, n, k, lda, ldb, ldc)
-        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {name}", flush=True)
-        assert name == want_name, name
-        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.75, A, lda, B, ldb, 1.5, C, ldc)
+        print(f"tall-skinny case {m}x{n}x{k} t{ta}{tb} -> {want_name}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -0.75, A, lda, B, ldb, 1.5, C, ldc,
+                      plan=want_name)
         want = run_oracle(0, ta, tb, m, n, k, -0.75, A, lda, B, ldb, 1.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
@@ -694,23 +672,19 @@ def test_tall_skinny_eight_wave_split_and_rounds(cuda, ta, tb):
 
 
 @pytest.mark.parametrize("dtype,m,n,k,ta,tb,kernel", [
-    (np.float32, 48, 70000, 1024, 0, 0, "mfma_f32_64x128x32_w2x2+splitk"),  # B 287 MB
-    (np.float32, 48, 70000, 1024, 1, 1, "mfma_f32_64x128x32_w2x2+splitk"),
+    (np.float32, 48, 70000, 1024, 0, 0, "mfma_f32_64x128x32_w2x2+splitk6"),  # B 287 MB
+    (np.float32, 48, 70000, 1024, 1, 1, "mfma_f32_64x128x32_w2x2+splitk6"),
     (np.float32, 64, 65536, 1024, 0, 1, "mfma_f32_64x256x32_w1x8"),         # B 268 MB
     (np.float64, 65536, 64, 1024, 0, 0, "mfma_f64_128x64x16_w2x2"),         # A 537 MB
     (np.float64, 65536, 40, 1024, 1, 0, "mfma_f64_128x64x16_w2x2"),
-    (np.float32, 70000, 64, 4096, 1, 0, "mfma_f32_256x64x32_w8x1+splitk"),  # A 1.15 GB
+    (np.float32, 70000, 64, 4096, 1, 0, "mfma_f32_256x64x32_w8x1+splitk11"),  # A 1.15 GB
 ])
 def test_streamed_operand_above_last_level_cache(cuda, dtype, m, n, k, ta, tb, kernel):
     """A grid one tile wide reads its long operand once; above 256 MiB that
     operand's loads are non-temporal (a kernel variant with the nt cache
-    policy, unsplit and with a split tail).  Every output against the oracle."""
-    import sushiblas_amd as sbx
-    lda, ldb = (m if ta else k), (k if tb else n)
-    name = sbx.gemm_select(sbx.F32 if dtype == np.float32 else sbx.F64, 0, ta, tb, m, n, k,
-                           lda, ldb, n)
-    assert name.startswith(kernel), name
-    err, _, _ = _case(cuda, dtype, 0, ta, tb, m, n, k, 1.0, 0.5, SEED + 83)
+    policy, unsplit and with a split tail), whichever plan runs; each runs by
+    name.  Every output against the oracle."""
+    err, _, _ = _case(cuda, dtype, 0, ta, tb, m, n, k, 1.0, 0.5, SEED + 83, plan=kernel)
     assert err <= TOL[dtype]
 
 
@@ -734,21 +708,20 @@ def test_split_k_is_deterministic(cuda, dtype):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_long_k_wide_splits(cuda, dtype):
-    """Small outputs over a long K: the tail is cut into up to 32 k-ranges
-    (256 x 256 x 65536: 16 tiles, 32 parts each), and the reduction sums up
-    to 32 partials per element in part order.  Ragged edges, padded leading
-    dimensions and a K tail on the second shape; whole results against the
-    oracle, the ldc padding untouched, two runs bit-identical."""
-    import sushiblas_amd as sbx
-    code = sbx.F32 if dtype == np.float32 else sbx.F64
-    for i, (m, n, k) in enumerate([(256, 256, 65536), (325, 351, 12266)]):
+    """Small outputs over a long K, run by name: the tail is cut into up to
+    32 k-ranges (256 x 256 x 65536: 16 64^2 tiles, 32 parts each; 325 x 351
+    x 12266: 36 tiles, 14 parts), and the reduction sums up to 32 partials
+    per element in part order.  Ragged edges, padded leading dimensions and
+    a K tail on the second shape; whole results against the oracle, the ldc
+    padding untouched, two runs bit-identical."""
+    tile = "mfma_f32_64x64x32_w2x2" if dtype == np.float32 else "mfma_f64_64x64x16_w2x2"
+    for i, (m, n, k, parts) in enumerate([(256, 256, 65536, 32), (325, 351, 12266, 14)]):
         A, lda, B, ldb, C, ldc = make_inputs(dtype, 0, 0, 0, m, n, k, SEED + 74 + i,
                                              pad=(3, 1, 5))
-        name = sbx.gemm_select(code, 0, 0, 0, m, n, k, lda, ldb, ldc)
-        print(f"long-K case {m}x{n}x{k} {np.dtype(dtype).name} -> {name}", flush=True)
-        assert "+splitk" in name and int(name.split("splitk")[1]) > 8, name
-        g1 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
-        g2 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
+        plan = f"{tile}+splitk{parts}"
+        print(f"long-K case {m}x{n}x{k} {np.dtype(dtype).name} -> {plan}", flush=True)
+        g1 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc, plan=plan)
+        g2 = run_sbx(cuda, dtype, 0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc, plan=plan)
         np.testing.assert_array_equal(g1.view(np.uint8), g2.view(np.uint8))
         want = run_oracle(0, 0, 0, m, n, k, 0.75, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, g1, want, m, n, ldc) <= TOL[dtype], (m, n, k)
@@ -764,11 +737,11 @@ def test_workspace_growth_under_concurrent_host_threads(cuda):
     import threading
     import torch
     import sushiblas_amd as sbx
-    shapes = [(512, 512, 512), (1920, 2816, 4096)]
-    # 15 x 22 = 330 tiles of 128x128, all short of one round, each cut into
-    # >= 3 parts of 64 KiB: > 32 MiB of partials
-    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 1920, 2816, 4096, 4096, 2816, 2816)
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 3, name
+    shapes = [(512, 512, 512), (3072, 3456, 2048)]
+    # 24 x 27 = 648 tiles of 128x128: a round of 512 and a 136-tile tail cut
+    # into >= 4 parts of 64 KiB: > 32 MiB of partials
+    name = sbx.gemm_select(sbx.F32, 0, 0, 0, 3072, 3456, 2048, 2048, 3456, 3456)
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and int(name.split("splitk")[1]) >= 4, name
     data = []
     for i, (m, n, k) in enumerate(shapes):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 72 + i)

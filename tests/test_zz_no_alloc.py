@@ -61,18 +61,19 @@ def test_noalloc_matches_gemm_ex_two_calls(cuda, dtype):
 
 
 def test_noalloc_bounds_the_split_to_the_scratch(cuda):
-    """A problem whose preferred split needs more than the scratch (330
-    tiles of 128x128 cut 3 ways: 62 MiB of partials) runs with a split
-    that fits; the result stays within tolerance of the oracle and of
-    sbx_gemm_ex.  A second, smaller call follows."""
+    """A problem whose preferred split needs more than the scratch (648
+    tiles of 128x128: a round of 512 and a 136-tile tail cut 4-5 ways, 34-42
+    MiB of partials) runs with a split that fits; the result stays within
+    tolerance of the oracle and of sbx_gemm_ex.  A second, smaller call
+    follows."""
     import torch
     import sushiblas_amd as sbx
     stream = torch.cuda.Stream()
-    m, n, k = 1920, 2816, 4096
+    m, n, k = 3072, 3456, 2048
     name = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
     parts = int(name.split("splitk")[1])
-    # 15 x 22 = 330 tiles, all short of one round
-    assert name.startswith("mfma_f32_128x128x16_w2x2+") and 330 * parts * 128 * 128 * 4 > SCRATCH, name
+    tail = (m // 128) * (n // 128) % 512  # 24 x 27 tiles, two per CU
+    assert name.startswith("mfma_f32_128x128x16_w2x2+") and tail * parts * 128 * 128 * 4 > SCRATCH, name
     for i, (mm, nn, kk) in enumerate([(m, n, k), (640, 640, 4096)]):
         ref, got, want, ldc = _run_both(cuda, np.float32, mm, nn, kk, 1.0, 0.5, SEED + 10 + i,
                                         stream)
