@@ -84,9 +84,9 @@ def parse():
     ap.add_argument("--regret-full", action="store_true",
                     help="keep every plan's measured and predicted time in the --regret rows")
     ap.add_argument("--k-sweep", action="store_true",
-                    help="with --probe: time 512 x 512 x K on the small-problem kernel for "
-                         "K = 512 ... 4096 (and K < 512 on its 4-wave form) and fit time = "
-                         "intercept + slope * K")
+                    help="with --probe: time 512 x 512 x K, K = 64 ... 2048, on both forms "
+                         "of the small-problem kernel (by name) and fit time = intercept + "
+                         "slope * K per form")
     return ap.parse_args()
 
 
@@ -579,29 +579,33 @@ def secondary_workloads(steps_arg, cpu_s=None):
 
 def k_sweep(steps):
     """512 x 512 x K (fp32, row-major, no transpose, alpha = 1, beta = 0) on
-    the kernel the library picks (the small-problem kernel, 8 waves from
-    K = 512 and 4 below, up to about K = 1800), with the probe build's stamps:
+    both forms of the small-problem kernel, run by name (sbx_gemm_ex_plan:
+    K cut over 8 waves and over 4), with the probe build's stamps:
     event-timed call time, the dispatch's span and the workgroups' phases;
-    time = intercept + slope * K fitted over each small-kernel form's rows."""
+    time = intercept + slope * K fitted over each form's rows.  Each row
+    also names the library's own pick for that K."""
     import numpy as np
     import torch
     import sushiblas_amd as sbx
     m = n = 512
     rows = []
-    for k in (64, 128, 192, 256, 384, 512, 640, 768, 1024, 1280, 1536, 1792):
+    for k in (64, 128, 192, 256, 384, 512, 640, 768, 1024, 1280, 1536, 2048):
         A = torch.empty(m * k, dtype=torch.float32, device="cuda")
         B = torch.empty(k * n, dtype=torch.float32, device="cuda")
         C = torch.zeros(m * n, dtype=torch.float32, device="cuda")
         sbx.fill_uniform(A, SEED + 1, 0)
         sbx.fill_uniform(B, SEED + 1, 1)
+        pick = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
+        for name in ("mfma_f32_32x32_ksplit8", "mfma_f32_32x32_ksplit4"):
 
-        def step():
-            sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0)
+            def step():
+                sbx.gemm_ex_plan(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0,
+                                 1, name)
 
-        probe = {"flops": 2.0 * m * n * k, "dtype": "f32"}
-        ms = time_launches(step, steps, 5, min_warm_s=0.25, probe=probe)
-        rows.append({"k": k, "kernel": sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n),
-                     "us": round(ms * 1e3, 3), "probe": probe.get("out")})
+            probe = {"flops": 2.0 * m * n * k, "dtype": "f32"}
+            ms = time_launches(step, steps, 5, min_warm_s=0.25, probe=probe)
+            rows.append({"k": k, "kernel": name, "pick": pick, "us": round(ms * 1e3, 3),
+                         "probe": probe.get("out")})
         del A, B, C
     fits = {}
     for form, name in (("8wave", "mfma_f32_32x32_ksplit8"), ("4wave", "mfma_f32_32x32_ksplit4")):

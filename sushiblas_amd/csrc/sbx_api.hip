@@ -740,6 +740,61 @@ bool parse_plan(const char* name, ForcedPlan* out)
     return false;
 }
 
+// The heuristics' last picks on this host thread.  A pick depends only on
+// what the key holds (the problem's shape, transposes and leading
+// dimensions, C's 16-byte alignment, whether a grouped table is used, the
+// algo, the workspace limit and the device), so a repeated call -- a serving
+// loop, a benchmark -- skips the model, about 2 us of host time per call.
+struct PlanKey {
+    int dev, dtype, algo, uplo;
+    bool ta, tb, c16, table;
+    int64_t m, n, k, lda, ldb, ldc, batch;
+    size_t max_ws;
+    bool operator==(const PlanKey& o) const
+    {
+        return dev == o.dev && dtype == o.dtype && algo == o.algo && uplo == o.uplo &&
+               ta == o.ta && tb == o.tb && c16 == o.c16 && table == o.table && m == o.m &&
+               n == o.n && k == o.k && lda == o.lda && ldb == o.ldb && ldc == o.ldc &&
+               batch == o.batch && max_ws == o.max_ws;
+    }
+};
+
+PlanKey plan_key(const Problem& p, int algo, size_t max_ws)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    return PlanKey{dev,   p.dtype, algo,  p.uplo, p.ta,  p.tb,  ((uintptr_t)p.C % 16) == 0,
+                   p.table != nullptr, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.batch, max_ws};
+}
+
+struct PlanCache {
+    static constexpr int kSlots = 8;
+    PlanKey key[kSlots];
+    Cfg cfg[kSlots];
+    SplitPlan sp[kSlots];
+    int used = 0, next = 0;
+
+    bool find(const PlanKey& k, Cfg* c, SplitPlan* s) const
+    {
+        for (int i = 0; i < used; ++i)
+            if (key[i] == k) {
+                *c = cfg[i];
+                *s = sp[i];
+                return true;
+            }
+        return false;
+    }
+    void put(const PlanKey& k, Cfg c, SplitPlan s)
+    {
+        key[next] = k;
+        cfg[next] = c;
+        sp[next] = s;
+        next = (next + 1) % kSlots;
+        if (used < kSlots) ++used;
+    }
+};
+thread_local PlanCache g_plan_cache;
+
 // fixed: the caller's split workspace; null: the stream's cached one.
 // forced: run this plan instead of the model's (SBX_UNSUPPORTED if the
 // problem cannot use it).
@@ -767,28 +822,32 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         cfg = forced->cfg;
         sp = ss.plan(forced->split);
     } else if (algo != SBX_ALGO_GENERIC) {
-        Cfg cands[kMaxCands];
-        const int64_t cus = cu_count();
         // no workspace for hipStreamPerThread: plan unsplit
         const size_t max_ws = fixed ? fixed->bytes : stream == hipStreamPerThread ? 0 : SIZE_MAX;
-        bool large = false;
-        const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
-        bool any = false;
-        Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
-        for (int i = 0; i < nc; ++i) {
-            if (!mfma_feasible(p, cands[i])) continue;
-            const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL ||
-                               cands[i] == F32_SMALL8;
-            if (algo == SBX_ALGO_MFMA_TILE && small) continue;
-            if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
-            const Choice c = model_plan(p, cands[i], cus, max_ws, large);
-            if (!any || c.seconds < best.seconds) best = c;  // ties keep the earlier candidate
-            any = true;
-        }
-        if (!any && algo != SBX_ALGO_AUTO) return SBX_UNSUPPORTED;
-        if (any) {
-            cfg = best.cfg;
-            sp = best.sp;
+        const PlanKey key = plan_key(p, algo, max_ws);
+        if (!g_plan_cache.find(key, &cfg, &sp)) {
+            Cfg cands[kMaxCands];
+            const int64_t cus = cu_count();
+            bool large = false;
+            const int nc = candidate_cfgs(p.dtype, p.m, p.n, p.uplo, cus, cands, &large);
+            bool any = false;
+            Choice best{GENERIC, SplitPlan{0, 1, 0}, 0.0};
+            for (int i = 0; i < nc; ++i) {
+                if (!mfma_feasible(p, cands[i])) continue;
+                const bool small = cands[i] == F32_SMALL || cands[i] == F64_SMALL ||
+                                   cands[i] == F32_SMALL8;
+                if (algo == SBX_ALGO_MFMA_TILE && small) continue;
+                if (algo == SBX_ALGO_MFMA_SMALL && !small) continue;
+                const Choice c = model_plan(p, cands[i], cus, max_ws, large);
+                if (!any || c.seconds < best.seconds) best = c;  // ties keep the earlier one
+                any = true;
+            }
+            if (!any && algo != SBX_ALGO_AUTO) return SBX_UNSUPPORTED;
+            if (any) {
+                cfg = best.cfg;
+                sp = best.sp;
+            }
+            g_plan_cache.put(key, cfg, sp);
         }
     }
     const CfgInfo& info = kCfg[cfg];
