@@ -90,3 +90,28 @@ def test_syrk_plans_the_triangle_cannot_use():
     for plan in ("mfma_f32_128x64x32_w2x2", "mfma_f32_32x32_ksplit4", "mfma_f64_128x128x16_w2x2"):
         assert _syrk_plan_call(plan) == 2, plan
     assert _syrk_plan_call("mfma_f32_128x128x16_w2x2", n=0) == 0
+
+
+def test_pick_cache_returns_what_the_model_picks():
+    """The per-thread cache of recent picks: cycling through more problems
+    than it holds (so entries are evicted and refilled), and through
+    problems that differ in one key field only, gives the same picks as a
+    first, cold pass, and sbx_gemm_plans (never cached) still holds each."""
+    shapes = [(sbx.F32, 0, 0, 0, m, n, k, 1) for m, n, k in
+              [(512, 512, 512), (513, 512, 512), (512, 513, 512), (512, 512, 513),
+               (8192, 8192, 8192), (65536, 64, 4096), (4095, 3001, 2047), (1536, 1536, 1024),
+               (300, 200, 5000), (1024, 1024, 1024), (2048, 2048, 2048)]]
+    shapes += [(sbx.F64, 0, 0, 0, 512, 512, 512, 1), (sbx.F32, 0, 1, 0, 512, 512, 512, 1),
+               (sbx.F32, 1, 0, 0, 512, 512, 512, 1), (sbx.F32, 0, 0, 0, 128, 128, 4096, 8)]
+    first = {}
+    for rep in range(3):
+        for sh in shapes:
+            dtype, layout, ta, tb, m, n, k, batch = sh
+            lda, ldb, ldc = _lds(layout, ta, tb, m, n, k)
+            pick = sbx.gemm_select(dtype, layout, ta, tb, m, n, k, lda, ldb, ldc, batch=batch)
+            if rep == 0:
+                first[sh] = pick
+                plans = [p for p, _ in sbx.gemm_plans(dtype, layout, ta, tb, m, n, k, lda, ldb,
+                                                      ldc, batch)]
+                assert pick in plans, (sh, pick)
+            assert pick == first[sh], (rep, sh, pick, first[sh])
