@@ -981,3 +981,25 @@ def test_split_k_on_two_streams(cuda):
     torch.cuda.synchronize()
     for o in outs:
         assert normwise(0, o.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32]
+
+
+def test_default_stream_is_torch_current_stream(cuda):
+    """A call without an explicit stream goes to torch's current stream,
+    including inside a `torch.cuda.stream` context (the raw-handle query
+    must agree with torch.cuda.current_stream())."""
+    import torch
+    import sushiblas_amd as sbx
+    assert sbx._stream(None) == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream()
+    m, n, k = 512, 512, 512
+    A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, 0, 0, m, n, k, SEED + 81)
+    want = run_oracle(0, 0, 0, m, n, k, 1.0, A, lda, B, ldb, 0.0, C, ldc)
+    dA = torch.from_numpy(A).to(cuda)
+    dB = torch.from_numpy(B).to(cuda)
+    out = torch.zeros(m * n, device=cuda)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        assert sbx._stream(None) == s.cuda_stream
+        sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, dA, lda, 0, dB, ldb, 0, 0.0, out, ldc, 0)
+    s.synchronize()
+    assert normwise(0, out.cpu().numpy(), want, m, n, ldc) <= TOL[np.float32]
