@@ -240,9 +240,10 @@ __device__ inline void probe_mark(const GemmArgs<T>& p, int point)
     // values as divergent and builds its buffer descriptors in VGPRs.  Every
     // lane of wave 0 then stores the same 16 bytes.
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    if (!p.stamps || wave != 0 || blockIdx.z != 0 || blockIdx.x >= (unsigned)p.stamp_blocks)
-        return;
-    unsigned long long* d = p.stamps + ((size_t)blockIdx.x * kStampPoints + point) * 2;
+    // workgroup index within batch entry 0 (the small-problem kernel's grid is 2-D)
+    const unsigned wg = blockIdx.x + blockIdx.y * gridDim.x;
+    if (!p.stamps || wave != 0 || blockIdx.z != 0 || wg >= (unsigned)p.stamp_blocks) return;
+    unsigned long long* d = p.stamps + ((size_t)wg * kStampPoints + point) * 2;
     const unsigned long long c = __builtin_amdgcn_s_memtime();
     const unsigned long long r = __builtin_amdgcn_s_memrealtime();
     d[0] = c;

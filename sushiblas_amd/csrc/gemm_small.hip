@@ -107,6 +107,26 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     static_assert(PART == kTile * kTile, "a wave's blocks cover the tile once");
     __shared__ T red[NW * PART];  // the waves' partial tiles
     probe_mark(p, 0);  // kernel entry
+
+    // Every kernel argument is read here, in one batch of scalar loads with
+    // one wait (the empty asm needs them all in registers at this point).
+    // Left to itself the compiler fetched them in three or four dependent
+    // rounds, each behind a branch on the previous round's values, and at
+    // kernel start every round is a trip to memory before the first operand
+    // load can be issued.
+    const T* A = p.A;
+    const T* B = p.B;
+    T* C = p.C;
+    const int64_t lda = p.lda, ldb = p.ldb, ldc = p.ldc;
+    const int64_t str_a = p.str_a, str_b = p.str_b, str_c = p.str_c;
+    const int M = p.M, N = p.N, K = p.K, relu = p.relu;
+    const T alpha = p.alpha, beta = p.beta;
+    const void* const* table = p.table;
+    const int table_swap = p.table_swap;
+    asm volatile("" ::"s"(A), "s"(B), "s"(C), "s"(lda), "s"(ldb), "s"(ldc), "s"(str_a),
+                 "s"(str_b), "s"(str_c), "s"(M), "s"(N), "s"(K), "s"(relu), "s"(alpha),
+                 "s"(beta), "s"(table), "s"(table_swap));
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // uniform per wave, and known to be: the buffer descriptors built from
@@ -114,36 +134,41 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     // over the distinct descriptors of the wave)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane % MB, q = lane / MB;
-    const int tm = (int)(blockIdx.x % (unsigned)p.tiles_m);
-    const int tn = (int)(blockIdx.x / (unsigned)p.tiles_m);
+    // grid (tiles_m, tiles_n, batch): no division by a kernel argument
+    const int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
     const int m0 = tm * kTile, n0 = tn * kTile;
-    const T* A;
-    const T* B;
-    T* C;
-    batch_bases(p, (int64_t)blockIdx.z, A, B, C);
+    const int64_t z = (int64_t)blockIdx.z;
+    if (table) {  // grouped launch: entry z's operands from the device table
+        const void* const* e = table + 3 * z;
+        A = static_cast<const T*>(e[table_swap ? 1 : 0]);
+        B = static_cast<const T*>(e[table_swap ? 0 : 1]);
+        C = static_cast<T*>(const_cast<void*>(e[2]));
+    } else {
+        A += z * str_a;
+        B += z * str_b;
+        C += z * str_c;
+    }
 
     // this wave's k groups [g0, g1) of the ceil(K/8); k past k_lim is zeroed
-    const int ng = (p.K + 7) / 8;
+    const int ng = (K + 7) / 8;
     const int g0 = (int)((int64_t)wave * ng / NW);
     const int g1 = (int)((int64_t)(wave + 1) * ng / NW);
-    const int k_lim = min(p.K, 8 * g1);
+    const int k_lim = min(K, 8 * g1);
 
     // operand origin (tile, k = 0) and the elements from there to the matrix end
-    const int64_t a_org = A_KC ? (int64_t)m0 * p.lda : (int64_t)m0;
-    const int64_t b_org = B_KC ? (int64_t)n0 * p.ldb : (int64_t)n0;
-    const int64_t a_end = A_KC ? (int64_t)(p.M - 1) * p.lda + p.K : (int64_t)(p.K - 1) * p.lda + p.M;
-    const int64_t b_end = B_KC ? (int64_t)(p.N - 1) * p.ldb + p.K : (int64_t)(p.K - 1) * p.ldb + p.N;
-    auto a_at = [&](int k0) { return a_org + (A_KC ? (int64_t)k0 : (int64_t)k0 * p.lda); };
-    auto b_at = [&](int k0) { return b_org + (B_KC ? (int64_t)k0 : (int64_t)k0 * p.ldb); };
+    const int64_t a_org = A_KC ? (int64_t)m0 * lda : (int64_t)m0;
+    const int64_t b_org = B_KC ? (int64_t)n0 * ldb : (int64_t)n0;
+    const int64_t a_end = A_KC ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M;
+    const int64_t b_end = B_KC ? (int64_t)(N - 1) * ldb + K : (int64_t)(K - 1) * ldb + N;
+    auto a_at = [&](int k0) { return a_org + (A_KC ? (int64_t)k0 : (int64_t)k0 * lda); };
+    auto b_at = [&](int k0) { return b_org + (B_KC ? (int64_t)k0 : (int64_t)k0 * ldb); };
 
     SmallOperand<T, A_KC, KTAIL> a[2];
     SmallOperand<T, B_KC, KTAIL> b[2];
     auto issue = [&](int st, int k0) {
         const int64_t pa = a_at(k0), pb = b_at(k0);
-        a[st].load(A + pa, (a_end - pa) * (int64_t)sizeof(T), p.lda, i, q, p.M - m0, k0, k_lim,
-                   p.K);
-        b[st].load(B + pb, (b_end - pb) * (int64_t)sizeof(T), p.ldb, i, q, p.N - n0, k0, k_lim,
-                   p.K);
+        a[st].load(A + pa, (a_end - pa) * (int64_t)sizeof(T), lda, i, q, M - m0, k0, k_lim, K);
+        b[st].load(B + pb, (b_end - pb) * (int64_t)sizeof(T), ldb, i, q, N - n0, k0, k_lim, K);
     };
 
     typename MF::acc_t acc[NB][NB];
@@ -204,7 +229,6 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
 
     // each lane finishes 1024 / (64 NW) elements of the 32x32 tile, summing
     // the waves' partials in wave order
-    const T alpha = p.alpha, beta = p.beta;
 #pragma unroll
     for (int u = 0; u < kTile * kTile / (NW * 64); ++u) {
         const int e = u * (NW * 64) + tid;
@@ -214,11 +238,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
         for (int w = 1; w < NW; ++w) sum += red[w * PART + e];
         const int row = (blk / NB) * MB + MF::row(r, el / MB), col = (blk % NB) * MB + el % MB;
         const int m = m0 + row, n = n0 + col;
-        if (m < p.M && n < p.N) {
-            T* cp = C + (int64_t)m * p.ldc + n;
+        if (m < M && n < N) {
+            T* cp = C + (int64_t)m * ldc + n;
             T v = alpha * sum;
             if (beta != (T)0) v += beta * *cp;
-            *cp = p.relu ? relu_of(v) : v;
+            *cp = relu ? relu_of(v) : v;
         }
     }
     probe_mark(p, 3);  // C stores issued
@@ -231,7 +255,7 @@ template <typename T, int NW>
 hipError_t launch_small_nw(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch,
                            hipStream_t stream)
 {
-    const dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)batch);
+    const dim3 grid((unsigned)a.tiles_m, (unsigned)a.tiles_n, (unsigned)batch);
     const dim3 block(NW * 64);
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
 #define SBX_LAUNCH(AK, BKC, TAIL) \

@@ -206,6 +206,9 @@ bool offsets_fit(bool kc, int tile_x, int bk, int64_t ld, size_t elem)
 bool mfma_feasible(const Problem& p, Cfg c)
 {
     const CfgInfo& ci = kCfg[c];
+    // the small-problem kernel's grid is (tiles along m, tiles along n, batch)
+    if ((c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8) && cdiv(p.n, ci.bn) > 65535)
+        return false;
     const size_t elem = p.dtype == SBX_F32 ? 4 : 8;
     return offsets_fit(!p.ta, ci.bm, ci.bk, p.lda, elem) &&
            offsets_fit(p.tb, ci.bn, ci.bk, p.ldb, elem) &&
@@ -814,9 +817,7 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
         if (p.uplo && forced->cfg != F32_256x256 && forced->cfg != F32_128x128 &&
             forced->cfg != F32_128x128_O3 && forced->cfg != F64_128x128)
             return SBX_UNSUPPORTED;
-        const bool tile = forced->cfg != GENERIC && forced->cfg != F32_SMALL &&
-                          forced->cfg != F64_SMALL && forced->cfg != F32_SMALL8;
-        if (tile && !mfma_feasible(p, forced->cfg)) return SBX_UNSUPPORTED;
+        if (forced->cfg != GENERIC && !mfma_feasible(p, forced->cfg)) return SBX_UNSUPPORTED;
         const SplitSpace ss = split_space(p, forced->cfg, cu_count());
         if (forced->split > 1 && forced->split > ss.smax) return SBX_UNSUPPORTED;
         cfg = forced->cfg;
@@ -1048,8 +1049,7 @@ int write_plans(const Problem& p, char* out, size_t cap)
     size_t used = 0;
     for (int i = 0; i < nc; ++i) {
         const Cfg c = cands[i];
-        const bool small = c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8;
-        if (!small && !mfma_feasible(p, c)) continue;
+        if (!mfma_feasible(p, c)) continue;
         const SplitSpace ss = split_space(p, c, cus);
         for (int j = -1; j < (int)(sizeof(kSplitSet) / sizeof(int)); ++j) {
             const int s = j < 0 ? 1 : kSplitSet[j];
