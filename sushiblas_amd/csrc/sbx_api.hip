@@ -225,17 +225,16 @@ int check_ld(int layout, bool trans, int64_t rows, int64_t cols, int64_t ld)
 
 // ---------------------------------------------------------------------------
 // Kernel choice and split-K: the candidate plan (tile config x split) with
-// the least modelled time.  The model's constants were fitted (bounded least
-// squares on log time, robust loss) to every candidate plan of 323 problems
-// timed on MI355X, 14008 plan timings: bench.py's regret_shapes(seed, 70)
-// for seeds 101, 102 and 103 (fp32 and fp64, both layouts and all four
-// transposes, a quarter of them batched, 1e8 .. 4e11 flops), 24 SYRK
-// problems of regret_syrk_shapes(101, 24), and 89 fixed problems (the
-// benchmark's shapes, the selection tests' shapes: large, tall, wide and
-// long-K ones, batches of small ones, SYRK).  Fitted on two of the random
-// seeds and the fixed problems,
-// the pick on the third seed was on average 1.4-3.3 % slower than the
-// fastest plan.
+// the least modelled time.  The tile configs' constants were fitted (bounded
+// least squares on log time, robust loss) to every candidate plan of 323
+// problems timed on MI355X, 14008 plan timings: bench.py's
+// regret_shapes(seed, 70) for seeds 101, 102 and 103 (fp32 and fp64, both
+// layouts and all four transposes, a quarter of them batched, 1e8 .. 4e11
+// flops), 24 SYRK problems of regret_syrk_shapes(101, 24), and 89 fixed
+// problems (the benchmark's shapes, the selection tests' shapes: large,
+// tall, wide and long-K ones, batches of small ones, SYRK).  The
+// small-problem kernel's terms were refitted later on their own (see
+// small_seconds).
 //   * a tile config keeps P workgroups per CU (its waves per SIMD); a
 //     workgroup's time is w = 2*BM*BN*K_part / (R * eff) + kTileSec +
 //     (C tile bytes) / kTileStoreBw, R per dtype, eff per config;
@@ -332,28 +331,32 @@ double cfg_eff(Cfg c)
 constexpr double kEpiSec = 2.2496e-13;
 
 // The small-problem kernel (one launch of 32x32 tiles, w = 2*32*32*K flops
-// each): a workgroup alone on a CU computes at kSmallRate; past one
-// workgroup per CU the CU's kSmallCuRate limits; fp64 at kSmallF64Rate and
-// kSmallF64CuRate of those.  Each workgroup adds kSmallWgSec, the launch
-// kSmallSec, and its operand bytes over kSmallBw (kSmallBwBatch for a batch,
-// whose entries' slabs are contiguous) bound it from below.
-constexpr double kSmallRate = 3.0164e11;
-constexpr double kSmallCuRate = 3.4791e11;
-constexpr double kSmallF64Rate = 0.7701;
-constexpr double kSmallF64CuRate = 0.5625;
-constexpr double kSmallBw = 4.4151e12;
-constexpr double kSmallBwBatch = 7.0462e12;
-constexpr double kSmallSec = 3.955e-6;
-constexpr double kSmallWgSec = 5.184e-7;
-constexpr double kSmall8 = 1.0819;  // the 8-wave form, relative to the 4-wave one
-// Its waves read operands straight from memory in the MFMA lane layout, so a
-// k-contiguous operand is read as one 16-byte run per row per lane and
-// touches many more cache lines per load than an x-contiguous one; the
-// factors by which the compute terms grow with k-contiguous operands:
-constexpr double kSmallLayF32Both = 1.0565;  // fp32, A and B (A or B alone: 1)
-constexpr double kSmallLayF64Both = 1.0430;
-constexpr double kSmallLayF64A = 1.1539;
-constexpr double kSmallLayF64B = 1.1529;
+// each), per form -- fp32 with K cut over 4 or 8 waves, fp64 over 4: a
+// launch cost `sec`; a workgroup alone on a CU computes at `rs`, up to `occ`
+// of them overlap on one CU, and past that the CU's rate `rc` limits; each
+// workgroup adds `wg`; the operand bytes over kSmallBw (kSmallBwBatch for a
+// batch, whose entries' slabs are contiguous) bound the time from below.
+// Its waves read operands straight from memory in the MFMA lane layout, so
+// the cost per k depends on which operands are k-contiguous: the layout
+// factors scale the flops per [A k-contiguous][B k-contiguous].
+// Fitted (robust least squares on log time, the tile constants above held)
+// to 16074 plan timings of 387 problems: regret_shapes(seed, 70) for seeds
+// 101-103, regret_shapes(seed, 60) for seeds 20261203 and 20261207, and the
+// 57 problems of the selection tests.  A plan's residual weighs more when
+// the plan is near its problem's fastest in measured time or in the fitted
+// model's prediction (refitted three times): a plan the model rates too
+// fast misleads the choice as much as the fastest rated too slow.
+struct SmallForm {
+    double sec, wg, rs, rc;
+    int occ;
+};
+constexpr SmallForm kSmallF32W4{2.4906e-06, 5.4829e-07, 2.8069e+11, 3.3576e+11, 2};
+constexpr SmallForm kSmallF32W8{2.3449e-06, 8.2063e-07, 1.0533e+12, 3.1181e+11, 1};
+constexpr SmallForm kSmallF64W4{2.8270e-06, 1.3501e-06, 1.9813e+11, 1.9291e+11, 2};
+constexpr double kSmallLayF32[2][2] = {{1.0, 1.1239}, {0.9675, 0.9678}};
+constexpr double kSmallLayF64[2][2] = {{1.0, 1.0845}, {1.1039, 0.8654}};
+constexpr double kSmallBw = 4.5425e+12;
+constexpr double kSmallBwBatch = 6.9315e+12;
 
 // The split-K space of a tile config: whole rounds run unsplit, and the
 // `rem` tiles of the tail (every tile of every entry, for a batch whose grid
@@ -400,23 +403,20 @@ size_t split_bytes(const Problem& p, Cfg c, const SplitSpace& ss, int64_t split)
 double small_seconds(const Problem& p, Cfg c, int64_t cus, const SplitSpace& ss)
 {
     const bool f64 = c == F64_SMALL;
-    const bool akc = !p.ta, bkc = p.tb;
-    const double lay = f64 ? (akc && bkc ? kSmallLayF64Both : akc ? kSmallLayF64A
-                                                        : bkc ? kSmallLayF64B : 1.0)
-                           : (akc && bkc ? kSmallLayF32Both : 1.0);
+    const SmallForm& f = f64 ? kSmallF64W4 : c == F32_SMALL8 ? kSmallF32W8 : kSmallF32W4;
+    const int akc = !p.ta, bkc = p.tb;
+    const double lay = f64 ? kSmallLayF64[akc][bkc] : kSmallLayF32[akc][bkc];
     const int64_t units = tile_count(p, c) * ss.nb;
-    const double w = 2.0 * 32 * 32 * (double)p.k;  // one workgroup's flops
-    const double lat = (double)cdiv(units, 2 * cus) *
-                       (w / (kSmallRate * (f64 ? kSmallF64Rate : 1.0)) + kSmallWgSec);
-    const double thr = (double)cdiv(units, cus) *
-                       (w / (kSmallCuRate * (f64 ? kSmallF64CuRate : 1.0)) + kSmallWgSec);
+    const double w = 2.0 * 32 * 32 * (double)p.k * lay;  // one workgroup's flops, layout-scaled
+    const double lat = (double)cdiv(units, f.occ * cus) * (w / f.rs + f.wg);
+    const double thr = (double)cdiv(units, cus) * (w / f.rc + f.wg);
     const double elem = f64 ? 8.0 : 4.0;
     const double bytes = ((double)p.m * p.k + (double)p.k * p.n + (double)p.m * p.n) * elem *
                          (double)ss.nb;
     const double stream = bytes / (p.batch > 1 ? kSmallBwBatch : kSmallBw);
-    const double compute = (lat > thr ? lat : thr) * lay;
-    const double t = kSmallSec + (compute > stream ? compute : stream);
-    return c == F32_SMALL8 ? t * kSmall8 : t;
+    double t = lat > thr ? lat : thr;
+    if (stream > t) t = stream;
+    return f.sec + t;
 }
 
 // Modelled seconds of config c with `split` k-ranges of its tail (1: none).
