@@ -98,8 +98,19 @@ struct SmallOperand {
     }
 };
 
+// The arguments the first operand loads depend on come first, as separate
+// scalars (14 dwords): this file is compiled with kernel-argument preloading,
+// so the dispatcher places them in SGPRs before the first instruction and
+// the loads go out without a trip to the argument buffer (a firmware without
+// preloading runs a compiled-in prologue that loads them instead).  `group`
+// is -1 for a strided launch, else the grouped launch's operand swap (0/1),
+// whose device table comes from p.  Everything the epilogue needs -- C, its
+// strides, the scalars -- is read from p after the k loop, so no wait for
+// it stands before the operand loads.
 template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL>
-__global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
+__global__ void __launch_bounds__(NW * 64)
+gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K, int group,
+                  int64_t str_a, int64_t str_b, GemmArgs<T> p)
 {
     typedef Mfma<T> MF;
     constexpr int MB = MF::MB, V = MF::V, NB = kTile / MB, NACC = MF::NACC;
@@ -107,25 +118,6 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     static_assert(PART == kTile * kTile, "a wave's blocks cover the tile once");
     __shared__ T red[NW * PART];  // the waves' partial tiles
     probe_mark(p, 0);  // kernel entry
-
-    // Every kernel argument is read here, in one batch of scalar loads with
-    // one wait (the empty asm needs them all in registers at this point).
-    // Left to itself the compiler fetched them in three or four dependent
-    // rounds, each behind a branch on the previous round's values, and at
-    // kernel start every round is a trip to memory before the first operand
-    // load can be issued.
-    const T* A = p.A;
-    const T* B = p.B;
-    T* C = p.C;
-    const int64_t lda = p.lda, ldb = p.ldb, ldc = p.ldc;
-    const int64_t str_a = p.str_a, str_b = p.str_b, str_c = p.str_c;
-    const int M = p.M, N = p.N, K = p.K, relu = p.relu;
-    const T alpha = p.alpha, beta = p.beta;
-    const void* const* table = p.table;
-    const int table_swap = p.table_swap;
-    asm volatile("" ::"s"(A), "s"(B), "s"(C), "s"(lda), "s"(ldb), "s"(ldc), "s"(str_a),
-                 "s"(str_b), "s"(str_c), "s"(M), "s"(N), "s"(K), "s"(relu), "s"(alpha),
-                 "s"(beta), "s"(table), "s"(table_swap));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -138,15 +130,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
     const int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
     const int m0 = tm * kTile, n0 = tn * kTile;
     const int64_t z = (int64_t)blockIdx.z;
-    if (table) {  // grouped launch: entry z's operands from the device table
-        const void* const* e = table + 3 * z;
-        A = static_cast<const T*>(e[table_swap ? 1 : 0]);
-        B = static_cast<const T*>(e[table_swap ? 0 : 1]);
-        C = static_cast<T*>(const_cast<void*>(e[2]));
+    if (group >= 0) {  // grouped launch: entry z's operands from the device table
+        const void* const* e = p.table + 3 * z;
+        A = static_cast<const T*>(e[group ? 1 : 0]);
+        B = static_cast<const T*>(e[group ? 0 : 1]);
     } else {
         A += z * str_a;
         B += z * str_b;
-        C += z * str_c;
     }
 
     // this wave's k groups [g0, g1) of the ceil(K/8); k past k_lim is zeroed
@@ -229,6 +219,10 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(GemmArgs<T> p)
 
     // each lane finishes 1024 / (64 NW) elements of the 32x32 tile, summing
     // the waves' partials in wave order
+    T* C = group >= 0 ? static_cast<T*>(const_cast<void*>(p.table[3 * z + 2])) : p.C + z * p.str_c;
+    const int64_t ldc = p.ldc;
+    const T alpha = p.alpha, beta = p.beta;
+    const int relu = p.relu;
 #pragma unroll
     for (int u = 0; u < kTile * kTile / (NW * 64); ++u) {
         const int e = u * (NW * 64) + tid;
@@ -257,9 +251,14 @@ hipError_t launch_small_nw(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch
 {
     const dim3 grid((unsigned)a.tiles_m, (unsigned)a.tiles_n, (unsigned)batch);
     const dim3 block(NW * 64);
+    // leading dimensions go in as 32-bit scalars (the planner's offset check
+    // keeps a 32-row tile's offsets, so ld itself, far below 2^31)
+    if (a.lda > INT32_MAX || a.ldb > INT32_MAX) return hipErrorInvalidValue;
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
 #define SBX_LAUNCH(AK, BKC, TAIL) \
-    gemm_small_kernel<T, NW, AK, BKC, TAIL><<<grid, block, 0, stream>>>(a)
+    gemm_small_kernel<T, NW, AK, BKC, TAIL><<<grid, block, 0, stream>>>(                  \
+        a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, a.table ? a.table_swap : -1, a.str_a,  \
+        a.str_b, a)
     if (a_kc && b_kc) {
         if (tail) SBX_LAUNCH(true, true, true);
         else SBX_LAUNCH(true, true, false);
