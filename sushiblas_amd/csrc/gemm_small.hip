@@ -2,11 +2,11 @@
 //
 // The MFMA tile kernel (gemm_mfma.hpp) fills the 256 CUs of a small problem
 // only by cutting K across workgroups, which costs a second kernel that sums
-// the parts.  Here each workgroup owns one 32x32 tile of C and its four
-// waves cut K four ways among themselves: every wave streams its k-range of
-// A and B straight from global memory into MFMA operand registers (no LDS
-// staging: the waves share no operand data), the four partial tiles meet in
-// LDS once, and the sum -- always wave 0 + 1 + 2 + 3, so the result is
+// the parts.  Here each workgroup owns one 32x32 tile of C and its NW = 4
+// or 8 waves cut K NW ways among themselves: every wave streams its k-range
+// of A and B straight from global memory into MFMA operand registers (no LDS
+// staging: the waves share no operand data), the NW partial tiles meet in
+// LDS once, and the sum -- always in wave order, so the result is
 // deterministic -- gets the alpha/beta (and ReLU) epilogue.  512^3 is 256
 // such tiles: one per CU.  fp32 runs one v_mfma_f32_32x32x2_f32 block per
 // wave; fp64 a 2x2 grid of v_mfma_f64_16x16x4_f64 blocks.
@@ -180,11 +180,14 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
                         acc[bi][bj] = MF::mma(a[st].v[bi][s][kk], b[st].v[bj][s][kk], acc[bi][bj]);
     };
 
-    // n stages of 32 k, two in flight (stage i in buffer i % 2).  Inside the
-    // loop the next stage is issued unconditionally; the last one or two
+    // n stages of 32 k in two register sets (stage i in set i % 2).  Inside
+    // the loop the next stage is issued unconditionally; the last one or two
     // stages are peeled so that nothing is loaded past the range (a load
     // whose result is never used still delays the epilogue, which reuses
-    // its registers, by a full memory round trip)
+    // its registers, by a full memory round trip).  The compiler places a
+    // stage's loads among the previous stage's MFMAs once their registers
+    // are free, so about one stage is in flight; pinning two (three register
+    // sets, loads between scheduling barriers) measured slower.
     const int ke = 8 * g1;
     int k0 = 8 * g0;
     const int n = (ke - k0 + 31) / 32;
