@@ -83,6 +83,10 @@ def parse():
                     help="SYRK shapes in the --regret list (regret_syrk_shapes)")
     ap.add_argument("--regret-full", action="store_true",
                     help="keep every plan's measured and predicted time in the --regret rows")
+    ap.add_argument("--abba", type=int, default=None, metavar="ROUNDS",
+                    help="interleaved timing of the tall-skinny call (configs[3]) against "
+                         "torch.addmm on the same buffers: ROUNDS rounds of four "
+                         "measurements in ABBA order, then the mirror")
     ap.add_argument("--k-sweep", action="store_true",
                     help="with --probe: time 512 x 512 x K, K = 64 ... 2048, on both forms "
                          "of the small-problem kernel (by name) and fit time = intercept + "
@@ -577,6 +581,48 @@ def secondary_workloads(steps_arg, cpu_s=None):
     return w
 
 
+def abba_tall_skinny(rounds, steps):
+    """This build's tall-skinny call and torch.addmm
+    (the vendor BLAS, TF32 off) on the same buffers, timed alternately in
+    one process: `rounds` rounds of four measurements of `steps`
+    back-to-back calls, in ABBA order (this build, vendor, vendor, this
+    build) and its mirror on alternate rounds, each after 50 ms of its own
+    warm-up, so that neither call always follows the other.  A single
+    sequential pair, as in the `also` line, can put either ahead when the
+    two are within the clock's run-to-run spread."""
+    import statistics
+    import torch
+    import sushiblas_amd as sbx
+    m, n, k = 65536, 64, 4096
+    A = torch.empty(m * k, device="cuda")
+    B = torch.empty(k * n, device="cuda")
+    C = torch.zeros(m * n, device="cuda")
+    sbx.fill_normal(A, SEED + 4, 0)
+    sbx.fill_normal(B, SEED + 4, 1, 1.0 / k ** 0.5)
+    A2, B2, C2 = A.view(m, k), B.view(k, n), C.view(m, n)
+    out = torch.empty(m, n, device="cuda")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    calls = {"sbx": lambda: sbx.gemm_ex(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0,
+                                        C, n, 0),
+             "vendor": lambda: torch.addmm(C2, A2, B2, beta=0.0, alpha=1.0, out=out)}
+    for fn in calls.values():
+        time_launches(fn, steps, 5, min_warm_s=0.5)
+    seq, res = [], {key: [] for key in calls}
+    for r in range(rounds):
+        order = ("sbx", "vendor", "vendor", "sbx") if r % 2 == 0 else ("vendor", "sbx", "sbx",
+                                                                        "vendor")
+        for key in order:
+            us = time_launches(calls[key], steps, 3, min_warm_s=0.05) * 1e3
+            res[key].append(us)
+            seq.append([key, round(us, 1)])
+    return {"workload": "fp32 65536x64x4096 (configs[3]): this build and torch.addmm, "
+                        "interleaved ABBA", "steps_per_measurement": steps,
+            "median_us": {key: round(statistics.median(v), 1) for key, v in res.items()},
+            "min_us": {key: round(min(v), 1) for key, v in res.items()},
+            "max_us": {key: round(max(v), 1) for key, v in res.items()},
+            "sequence_us": seq}
+
+
 def k_sweep(steps):
     """512 x 512 x K (fp32, row-major, no transpose, alpha = 1, beta = 0) on
     both forms of the small-problem kernel, run by name (sbx_gemm_ex_plan:
@@ -809,6 +855,9 @@ def main():
         sbx.lib()
         print(json.dumps(regret(args.regret, args.regret_count, args.regret_full,
                                 args.regret_syrk)), flush=True)
+        return
+    if args.abba is not None:
+        print(json.dumps(abba_tall_skinny(max(1, args.abba), args.steps)), flush=True)
         return
     if args.k_sweep:
         if not args.probe:
