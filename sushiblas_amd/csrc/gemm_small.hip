@@ -26,7 +26,16 @@ namespace sbx {
 namespace {
 
 constexpr int kTile = 32;        // workgroup tile edge
-constexpr int kStageGroups = 4;  // k groups of 8 per pipeline stage (32 k)
+// k groups of 8 per pipeline stage, per form: 32 k for the 4-wave form, 16 k
+// for the 8-wave one, whose waves each hold half as much K (timed in
+// rotation at 512^2 x K, results bit-identical: the 8-wave form 5 % faster
+// at K = 512 and 16 % at K = 2048 with 16-k stages; the 4-wave form no
+// faster from K = 512 on, with 16 or with 64)
+template <int NW>
+constexpr int stage_groups()
+{
+    return NW == 8 ? 2 : 4;
+}
 
 // One element of T from a raw buffer load (4 or 8 bytes).
 __device__ inline float load_elem(float*, __amdgpu_buffer_rsrc_t r, int off)
@@ -39,14 +48,14 @@ __device__ inline double load_elem(double*, __amdgpu_buffer_rsrc_t r, int off)
     return __hiloint2double((int)w.y, (int)w.x);
 }
 
-// One operand's registers for a stage of 32 k values: for block b (of NB
+// One operand's registers for a stage of SG groups of 8 k values: for block b (of NB
 // along the operand's m or n), group s and step kk, v[b][s][kk] is this
 // lane's element (row/column b*MB + lane % MB of the tile).
-template <typename T, bool KC, bool KTAIL>
+template <typename T, bool KC, bool KTAIL, int SG>
 struct SmallOperand {
     typedef Mfma<T> MF;
     static constexpr int MB = MF::MB, V = MF::V, NB = kTile / MB;
-    T v[NB][kStageGroups][V];
+    T v[NB][SG][V];
 
     // base: the operand at this stage's first k (k0) and the tile's first
     // row (KC: element (x, k) at x*ld + k; else (k, x) at k*ld + x).
@@ -60,7 +69,7 @@ struct SmallOperand {
         for (int b = 0; b < NB; ++b) {
             const int x = b * MB + i;
 #pragma unroll
-            for (int s = 0; s < kStageGroups; ++s) {
+            for (int s = 0; s < SG; ++s) {
                 const int kq = 8 * s + V * q;  // first k of this lane's run, stage-relative
                 if (KC) {
                     const bool ok = x < x_rem && k0 + kq < k_lim;
@@ -153,8 +162,10 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     auto a_at = [&](int k0) { return a_org + (A_KC ? (int64_t)k0 : (int64_t)k0 * lda); };
     auto b_at = [&](int k0) { return b_org + (B_KC ? (int64_t)k0 : (int64_t)k0 * ldb); };
 
-    SmallOperand<T, A_KC, KTAIL> a[2];
-    SmallOperand<T, B_KC, KTAIL> b[2];
+    constexpr int SG = stage_groups<NW>();
+    constexpr int kStageK = 8 * SG;  // k values per stage
+    SmallOperand<T, A_KC, KTAIL, SG> a[2];
+    SmallOperand<T, B_KC, KTAIL, SG> b[2];
     auto issue = [&](int st, int k0) {
         const int64_t pa = a_at(k0), pb = b_at(k0);
         a[st].load(A + pa, (a_end - pa) * (int64_t)sizeof(T), lda, i, q, M - m0, k0, k_lim, K);
@@ -170,7 +181,7 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
             for (int r = 0; r < NACC; ++r) acc[bi][bj][r] = 0;
     auto mma = [&](int st) {
 #pragma unroll
-        for (int s = 0; s < kStageGroups; ++s)
+        for (int s = 0; s < SG; ++s)
 #pragma unroll
             for (int kk = 0; kk < V; ++kk)
 #pragma unroll
@@ -180,7 +191,7 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
                         acc[bi][bj] = MF::mma(a[st].v[bi][s][kk], b[st].v[bj][s][kk], acc[bi][bj]);
     };
 
-    // n stages of 32 k in two register sets (stage i in set i % 2).  Inside
+    // n stages of kStageK k in two register sets (stage i in set i % 2).  Inside
     // the loop the next stage is issued unconditionally; the last one or two
     // stages are peeled so that nothing is loaded past the range (a load
     // whose result is never used still delays the epilogue, which reuses
@@ -190,19 +201,19 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     // sets, loads between scheduling barriers) measured slower.
     const int ke = 8 * g1;
     int k0 = 8 * g0;
-    const int n = (ke - k0 + 31) / 32;
+    const int n = (ke - k0 + kStageK - 1) / kStageK;
     if (n > 0) issue(0, k0);
     probe_mark(p, 1);  // first stage's loads issued
     int done = 0;  // stages consumed
     for (; done + 2 < n; done += 2) {
-        issue(1, k0 + 32);
+        issue(1, k0 + kStageK);
         mma(0);
-        issue(0, k0 + 64);
+        issue(0, k0 + 2 * kStageK);
         mma(1);
-        k0 += 64;
+        k0 += 2 * kStageK;
     }
     if (n - done == 2) {
-        issue(1, k0 + 32);
+        issue(1, k0 + kStageK);
         mma(0);
         mma(1);
     } else if (n - done == 1) {
