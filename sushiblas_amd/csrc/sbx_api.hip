@@ -340,23 +340,25 @@ constexpr double kEpiSec = 2.2496e-13;
 // the cost per k depends on which operands are k-contiguous: the layout
 // factors scale the flops per [A k-contiguous][B k-contiguous].
 // Fitted (robust least squares on log time, the tile constants above held)
-// to 16074 plan timings of 387 problems: regret_shapes(seed, 70) for seeds
-// 101-103, regret_shapes(seed, 60) for seeds 20261203 and 20261207, and the
-// 57 problems of the selection tests.  A plan's residual weighs more when
-// the plan is near its problem's fastest in measured time or in the fitted
-// model's prediction (refitted three times): a plan the model rates too
-// fast misleads the choice as much as the fastest rated too slow.
+// to 21,000 plan timings of 637 problems, timed on the kernel as it is:
+// regret_shapes(seed, 70) for seeds 101-103, regret_shapes(seed, 60) for
+// seeds 20261203, 20261207, 20261209 and 20261211, the 57 problems of the
+// selection tests and 110 problems with one side of 48-512 and the other of
+// 512-8192.  A plan's residual weighs more when the plan is near its
+// problem's fastest in measured time or in the fitted model's prediction
+// (refitted three times): a plan the model rates too fast misleads the
+// choice as much as the fastest rated too slow.
 struct SmallForm {
     double sec, wg, rs, rc;
     int occ;
 };
-constexpr SmallForm kSmallF32W4{2.4906e-06, 5.4829e-07, 2.8069e+11, 3.3576e+11, 2};
-constexpr SmallForm kSmallF32W8{2.3449e-06, 8.2063e-07, 1.0533e+12, 3.1181e+11, 1};
-constexpr SmallForm kSmallF64W4{2.8270e-06, 1.3501e-06, 1.9813e+11, 1.9291e+11, 2};
-constexpr double kSmallLayF32[2][2] = {{1.0, 1.1239}, {0.9675, 0.9678}};
-constexpr double kSmallLayF64[2][2] = {{1.0, 1.0845}, {1.1039, 0.8654}};
-constexpr double kSmallBw = 4.5425e+12;
-constexpr double kSmallBwBatch = 6.9315e+12;
+constexpr SmallForm kSmallF32W4{2.8336e-06, 4.5870e-07, 2.9187e+11, 3.4076e+11, 2};
+constexpr SmallForm kSmallF32W8{2.7012e-06, 5.0971e-07, 4.8464e+11, 3.5333e+11, 1};
+constexpr SmallForm kSmallF64W4{3.1395e-06, 1.0982e-06, 4.2042e+11, 1.8879e+11, 2};
+constexpr double kSmallLayF32[2][2] = {{1.0, 1.0856}, {0.9772, 1.0096}};
+constexpr double kSmallLayF64[2][2] = {{1.0, 1.0486}, {1.0604, 0.9434}};
+constexpr double kSmallBw = 4.5975e+12;
+constexpr double kSmallBwBatch = 7.1474e+12;
 
 // The split-K space of a tile config: whole rounds run unsplit, and the
 // `rem` tiles of the tail (every tile of every entry, for a batch whose grid
