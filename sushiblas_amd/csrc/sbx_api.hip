@@ -340,7 +340,7 @@ constexpr double kEpiSec = 2.2496e-13;
 // the cost per k depends on which operands are k-contiguous: the layout
 // factors scale the flops per [A k-contiguous][B k-contiguous].
 // Fitted (robust least squares on log time, the tile constants above held)
-// to 21,000 plan timings of 637 problems, timed on the kernel as it is:
+// to 28,488 plan timings of 617 problems, timed on the kernel as it is:
 // regret_shapes(seed, 70) for seeds 101-103, regret_shapes(seed, 60) for
 // seeds 20261203, 20261207, 20261209 and 20261211, the 57 problems of the
 // selection tests and 110 problems with one side of 48-512 and the other of
