@@ -83,6 +83,9 @@ def parse():
                     help="SYRK shapes in the --regret list (regret_syrk_shapes)")
     ap.add_argument("--regret-full", action="store_true",
                     help="keep every plan's measured and predicted time in the --regret rows")
+    ap.add_argument("--hbm-rates", action="store_true",
+                    help="time torch's copy and sum over 1 GiB: the HBM rates of the vendor's "
+                         "own streaming kernels on this box")
     ap.add_argument("--abba", type=int, default=None, metavar="ROUNDS",
                     help="interleaved timing of the tall-skinny call (configs[3]) against "
                          "torch.addmm on the same buffers: ROUNDS rounds of four "
@@ -104,6 +107,23 @@ def calibrate_copy():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calibrate_copy_bytes": n * 4, "dispatches": 3}), flush=True)
+
+
+def hbm_rates():
+    """The HBM rates the vendor's own streaming kernels reach on this box,
+    timed like the workloads over 1 GiB of fp32: torch's copy (read +
+    write) and torch.sum (read only) -- practical ceilings beside the 8 TB/s
+    datasheet figure, for the HBM-bound rows (GEMV)."""
+    import torch
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    acc = torch.empty((), dtype=torch.float32, device="cuda")
+    copy_ms = time_launches(lambda: dst.copy_(src), 20, 3, min_warm_s=0.25)
+    sum_ms = time_launches(lambda: torch.sum(src, dim=(0,), out=acc), 20, 3, min_warm_s=0.25)
+    return {"bytes": n * 4, "copy_ms": round(copy_ms, 4),
+            "copy_gbs": round(2 * n * 4 / (copy_ms * 1e-3) / 1e9, 1),
+            "sum_ms": round(sum_ms, 4), "sum_read_gbs": round(n * 4 / (sum_ms * 1e-3) / 1e9, 1)}
 
 
 PROBE = False  # --probe: record per-workgroup clock stamps of the timed dispatches
@@ -855,6 +875,9 @@ def main():
         sbx.lib()
         print(json.dumps(regret(args.regret, args.regret_count, args.regret_full,
                                 args.regret_syrk)), flush=True)
+        return
+    if args.hbm_rates:
+        print(json.dumps(hbm_rates()), flush=True)
         return
     if args.abba is not None:
         print(json.dumps(abba_tall_skinny(max(1, args.abba), args.steps)), flush=True)
