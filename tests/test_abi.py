@@ -179,6 +179,24 @@ def test_syrk_selection(dtype, n, k, expect):
     assert sbx.syrk_select(dtype, 1, 1, 1, n, k, k, n) == expect
 
 
+def test_small_kernel_grid_limit():
+    """The small-problem kernel's grid is (tiles along m, tiles along n,
+    batch): past 65535 tiles of 32 along n it is not a candidate, and a plan
+    that forces it is refused rather than launched."""
+    def small(n):
+        return [p for p, _ in sbx.gemm_plans(sbx.F32, 0, 0, 0, 32, n, 8, 8, n, n, 1)
+                if "ksplit" in p]
+    assert small(65535 * 32) == ["mfma_f32_32x32_ksplit4", "mfma_f32_32x32_ksplit8"]
+    assert small(65535 * 32 + 1) == []
+    n = 65535 * 32 + 1
+    assert not sbx.gemm_select(0, 0, 0, 0, 32, n, 8, 8, n, n).startswith("mfma_f32_32x32_ksplit")
+    # forcing it: refused on the host, before any HIP call (placeholder pointers)
+    a = ctypes.c_float(1.0)
+    st = sbx.lib().sbx_gemm_ex_plan(0, 0, 0, 0, 0, 32, n, 8, ctypes.byref(a), 16, 8, 0, 16, n, 0,
+                                    ctypes.byref(a), 16, n, 0, 1, b"mfma_f32_32x32_ksplit4")
+    assert st == 2, st
+
+
 def test_huge_leading_dimension_falls_back_to_generic():
     """A tile whose 32-bit buffer offsets would overflow goes to the generic kernel."""
     assert sbx.gemm_select(0, 0, 0, 0, 1024, 1024, 1024, 1 << 24, 1024, 1024) == \
