@@ -2,8 +2,8 @@
 //
 // The MFMA tile kernel (gemm_mfma.hpp) fills the 256 CUs of a small problem
 // only by cutting K across workgroups, which costs a second kernel that sums
-// the parts.  Here each workgroup owns one 32x32 tile of C and its NW = 4
-// or 8 waves cut K NW ways among themselves: every wave streams its k-range
+// the parts.  Here each workgroup owns one 32x32 tile of C and its NW = 4,
+// 8 or 16 waves cut K NW ways among themselves: every wave streams its k-range
 // of A and B straight from global memory into MFMA operand registers (no LDS
 // staging: the waves share no operand data), the NW partial tiles meet in
 // LDS once, and the sum -- always in wave order, so the result is
@@ -27,14 +27,15 @@ namespace {
 
 constexpr int kTile = 32;        // workgroup tile edge
 // k groups of 8 per pipeline stage, per form: 32 k for the 4-wave form, 16 k
-// for the 8-wave one, whose waves each hold half as much K (timed in
-// rotation at 512^2 x K, results bit-identical: the 8-wave form 5 % faster
-// at K = 512 and 16 % at K = 2048 with 16-k stages; the 4-wave form no
-// faster from K = 512 on, with 16 or with 64)
+// for the 8- and 16-wave ones, whose waves each hold a half or a quarter as
+// much K (timed in rotation at 512^2 x K: the 8-wave form ran 5 % faster at
+// K = 512 and 16 % at K = 2048 with 16-k stages than with 32, bit-identical;
+// the 16-wave form 5-14 % slower with 8-k stages than with 16 from K = 512
+// on; the 4-wave form no faster from K = 512 on, with 16 or with 64)
 template <int NW>
 constexpr int stage_groups()
 {
-    return NW == 8 ? 2 : 4;
+    return NW >= 8 ? 2 : 4;
 }
 
 // One element of T from a raw buffer load (4 or 8 bytes).
@@ -135,8 +136,33 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     // over the distinct descriptors of the wave)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane % MB, q = lane / MB;
-    // grid (tiles_m, tiles_n, batch): no division by a kernel argument
-    const int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
+    // grid (tiles_m, tiles_n, batch).  The hardware deals workgroups to the
+    // 8 XCDs round-robin by linear index, each XCD with its own L2.  When an
+    // entry's tile count is a multiple of 8 (so that every entry deals
+    // alike), the tiles are renumbered so that XCD j takes the j-th eighth of
+    // them, walked in columns G tiles tall: an XCD then covers about a
+    // sqrt(tiles / 8)-wide square, whose A and B panels its L2 shares,
+    // instead of every column of tiles (512^2 x 2048: 17.6 against 21.2 us
+    // on the 4-wave form, 12.9 against 14.0 on the 16-wave one)
+    int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
+    {
+        const unsigned gx = (unsigned)(M + kTile - 1) / kTile;  // gridDim.x
+        const unsigned gy = (unsigned)(N + kTile - 1) / kTile;  // gridDim.y
+        const unsigned tiles = gx * gy;
+        if ((tiles & 7u) == 0 && tiles > 8) {
+            const unsigned lin = (unsigned)tm + gx * (unsigned)tn;
+            const unsigned eighth = tiles >> 3;
+            const unsigned id = (lin & 7u) * eighth + (lin >> 3);
+            const unsigned G = 1u << ((31 - __builtin_clz(eighth)) >> 1);  // ~sqrt(eighth)
+            const unsigned span = G * gy;
+            const unsigned grp = id / span;
+            const unsigned first = grp * G;
+            const unsigned gs = min(gx - first, G);
+            const unsigned in = id - grp * span;
+            tm = (int)(first + in % gs);
+            tn = (int)(in / gs);
+        }
+    }
     const int m0 = tm * kTile, n0 = tn * kTile;
     const int64_t z = (int64_t)blockIdx.z;
     if (group >= 0) {  // grouped launch: entry z's operands from the device table
@@ -294,8 +320,13 @@ template <typename T>
 hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream,
                         int waves)
 {
-    if (waves == 8) return launch_small_nw<T, 8>(a, a_kc, b_kc, batch, stream);
-    return launch_small_nw<T, 4>(a, a_kc, b_kc, batch, stream);
+    if (waves == 4) return launch_small_nw<T, 4>(a, a_kc, b_kc, batch, stream);
+    // 8 and 16 waves: fp32 only (16 fp64 partial tiles would take 128 KB of LDS)
+    if constexpr (sizeof(T) == 4) {
+        if (waves == 8) return launch_small_nw<T, 8>(a, a_kc, b_kc, batch, stream);
+        if (waves == 16) return launch_small_nw<T, 16>(a, a_kc, b_kc, batch, stream);
+    }
+    return hipErrorInvalidValue;
 }
 
 template hipError_t launch_small<float>(const GemmArgs<float>&, bool, bool, int, hipStream_t, int);

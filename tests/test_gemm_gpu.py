@@ -414,24 +414,71 @@ def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
         assert err <= TOL[np.float32], (m, n, k, plan)
 
 
-# -- the small-problem kernel with K cut over 8 waves ---------------------------
+# -- the small-problem kernel with K cut over 8 or 16 waves ---------------------
 
+@pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit8", "mfma_f32_32x32_ksplit16"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_small_kernel_eight_waves(cuda, ta, tb):
-    """The small-problem kernel's 8-wave form, run by name: 512^3, and a
-    ragged 300 x 200 x 1001 with padded leading dimensions and misaligned
-    bases (K tail, partial tiles); C outside the window untouched."""
-    plan = "mfma_f32_32x32_ksplit8"
+def test_small_kernel_more_waves(cuda, ta, tb, plan):
+    """The small-problem kernel's 8- and 16-wave forms, run by name: 512^3,
+    and a ragged 300 x 200 x 1001 with padded leading dimensions and
+    misaligned bases (K tail, partial tiles); C outside the window
+    untouched."""
     for i, (m, n, k, pad, off) in enumerate([(512, 512, 512, (0, 0, 0), (0, 0, 0)),
                                              (300, 200, 1001, (3, 1, 5), (1, 2, 3))]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i, pad)
-        print(f"eight-wave case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        print(f"small-kernel case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
         got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc,
                       offsets=off, plan=plan)
         want = run_oracle(0, ta, tb, m, n, k, -1.5, A, lda, B, ldb, 0.5, C, ldc)
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k)
         outside = (np.arange(C.size) % ldc) >= n
         np.testing.assert_array_equal(got[outside], C[outside])
+
+
+@pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit4", "mfma_f32_32x32_ksplit8",
+                                  "mfma_f32_32x32_ksplit16"])
+def test_small_kernel_tile_order(cuda, plan):
+    """Shapes whose tile count is a multiple of 8, where the small-problem
+    kernel renumbers its tiles XCD by XCD in columns G tiles tall: 16 x 16
+    tiles (G = 4), 9 x 8 ragged tiles (G = 2, the last column group one tile
+    tall), 2 x 128 (a group taller than the matrix), each with a transposed
+    operand; then a strided batch of 3 entries of 2 x 8 tiles.  Every tile
+    of C matches the oracle and C's padding is untouched, so no tile is
+    skipped or written twice."""
+    import torch
+    import sushiblas_amd as sbx
+    for i, (m, n, k, ta, tb) in enumerate([(512, 512, 701, 0, 0), (283, 253, 300, 0, 1),
+                                           (283, 253, 300, 1, 0), (64, 4096, 256, 0, 0),
+                                           (64, 4096, 256, 1, 1)]):
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 95 + i,
+                                             pad=(1, 2, 3))
+        print(f"tile-order case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        got = run_sbx(cuda, np.float32, 0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -0.5, C, ldc,
+                      plan=plan)
+        want = run_oracle(0, ta, tb, m, n, k, 0.75, A, lda, B, ldb, -0.5, C, ldc)
+        assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k, ta, tb)
+        outside = (np.arange(C.size) % ldc) >= n
+        np.testing.assert_array_equal(got[outside], C[outside])
+    batch, m, n, k = 3, 64, 256, 200
+    str_a, str_b, str_c = m * k + 5, k * n + 3, m * n + 7
+    A = oracle.fill_uniform(batch * str_a, np.float32, SEED + 99, 0)
+    B = oracle.fill_uniform(batch * str_b, np.float32, SEED + 99, 1)
+    C = oracle.fill_uniform(batch * str_c, np.float32, SEED + 99, 2)
+    dA, dB, dC = (torch.from_numpy(x).to(cuda) for x in (A, B, C))
+    print(f"tile-order case batch {batch} x {m}x{n}x{k} -> {plan}", flush=True)
+    sbx.gemm_ex_plan(sbx.F32, 0, 0, 0, m, n, k, 1.25, dA, k, str_a, dB, n, str_b, 0.5, dC, n,
+                     str_c, batch, plan)
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    want = C.copy()
+    oracle.gemm_strided_batched(0, 0, 0, m, n, k, 1.25, A, k, str_a, B, n, str_b, 0.5, want, n,
+                                str_c, batch, 1)
+    for b in range(batch):
+        g = c_window(0, got[b * str_c:b * str_c + m * n], m, n, n)
+        w = c_window(0, want[b * str_c:b * str_c + m * n], m, n, n)
+        assert oracle.rel_fro_err(g, w) <= TOL[np.float32], b
+        np.testing.assert_array_equal(got[b * str_c + m * n:(b + 1) * str_c],
+                                      C[b * str_c + m * n:(b + 1) * str_c])
 
 
 # -- the large fp32 tiles on ragged edges --------------------------------------
