@@ -646,7 +646,7 @@ def abba_tall_skinny(rounds, steps):
 def k_sweep(steps):
     """512 x 512 x K (fp32, row-major, no transpose, alpha = 1, beta = 0) on
     both forms of the small-problem kernel, run by name (sbx_gemm_ex_plan:
-    K cut over 4, 8 and 16 waves), with the probe build's stamps:
+    K cut over 8 waves and over 4), with the probe build's stamps:
     event-timed call time, the dispatch's span and the workgroups' phases;
     time = intercept + slope * K fitted over each form's rows.  Each row
     also names the library's own pick for that K."""
@@ -662,8 +662,7 @@ def k_sweep(steps):
         sbx.fill_uniform(A, SEED + 1, 0)
         sbx.fill_uniform(B, SEED + 1, 1)
         pick = sbx.gemm_select(sbx.F32, 0, 0, 0, m, n, k, k, n, n)
-        for name in ("mfma_f32_32x32_ksplit16", "mfma_f32_32x32_ksplit8",
-                     "mfma_f32_32x32_ksplit4"):
+        for name in ("mfma_f32_32x32_ksplit8", "mfma_f32_32x32_ksplit4"):
 
             def step():
                 sbx.gemm_ex_plan(sbx.F32, 0, 0, 0, m, n, k, 1.0, A, k, 0, B, n, 0, 0.0, C, n, 0,
@@ -675,8 +674,7 @@ def k_sweep(steps):
                          "probe": probe.get("out")})
         del A, B, C
     fits = {}
-    for form, name in (("16wave", "mfma_f32_32x32_ksplit16"), ("8wave", "mfma_f32_32x32_ksplit8"),
-                       ("4wave", "mfma_f32_32x32_ksplit4")):
+    for form, name in (("8wave", "mfma_f32_32x32_ksplit8"), ("4wave", "mfma_f32_32x32_ksplit4")):
         pts = [r for r in rows if r["kernel"] == name and r["probe"]]
         if len(pts) < 2:
             continue

@@ -2,8 +2,8 @@
 //
 // The MFMA tile kernel (gemm_mfma.hpp) fills the 256 CUs of a small problem
 // only by cutting K across workgroups, which costs a second kernel that sums
-// the parts.  Here each workgroup owns one 32x32 tile of C and its NW = 4,
-// 8 or 16 waves cut K NW ways among themselves: every wave streams its k-range
+// the parts.  Here each workgroup owns one 32x32 tile of C and its NW = 4
+// or 8 waves cut K NW ways among themselves: every wave streams its k-range
 // of A and B straight from global memory into MFMA operand registers (no LDS
 // staging: the waves share no operand data), the NW partial tiles meet in
 // LDS once, and the sum -- always in wave order, so the result is
@@ -27,15 +27,14 @@ namespace {
 
 constexpr int kTile = 32;        // workgroup tile edge
 // k groups of 8 per pipeline stage, per form: 32 k for the 4-wave form, 16 k
-// for the 8- and 16-wave ones, whose waves each hold a half or a quarter as
-// much K (timed in rotation at 512^2 x K: the 8-wave form ran 5 % faster at
-// K = 512 and 16 % at K = 2048 with 16-k stages than with 32, bit-identical;
-// the 16-wave form 5-14 % slower with 8-k stages than with 16 from K = 512
-// on; the 4-wave form no faster from K = 512 on, with 16 or with 64)
+// for the 8-wave one, whose waves each hold half as much K (timed in
+// rotation at 512^2 x K, results bit-identical: the 8-wave form 5 % faster
+// at K = 512 and 16 % at K = 2048 with 16-k stages; the 4-wave form no
+// faster from K = 512 on, with 16 or with 64)
 template <int NW>
 constexpr int stage_groups()
 {
-    return NW >= 8 ? 2 : 4;
+    return NW == 8 ? 2 : 4;
 }
 
 // One element of T from a raw buffer load (4 or 8 bytes).
@@ -142,8 +141,8 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     // alike), the tiles are renumbered so that XCD j takes the j-th eighth of
     // them, walked in columns G tiles tall: an XCD then covers about a
     // sqrt(tiles / 8)-wide square, whose A and B panels its L2 shares,
-    // instead of every column of tiles (512^2 x 2048: 17.6 against 21.2 us
-    // on the 4-wave form, 12.9 against 14.0 on the 16-wave one)
+    // instead of every column of tiles (512^2 x 2048: 17.9 against 21.2 us
+    // on the 4-wave form, 14.5 against 15.5 on the 8-wave one)
     int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
     {
         const unsigned gx = (unsigned)(M + kTile - 1) / kTile;  // gridDim.x
@@ -321,10 +320,9 @@ hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, h
                         int waves)
 {
     if (waves == 4) return launch_small_nw<T, 4>(a, a_kc, b_kc, batch, stream);
-    // 8 and 16 waves: fp32 only (16 fp64 partial tiles would take 128 KB of LDS)
+    // 8 waves: fp32 only (the planner offers no fp64 form of it)
     if constexpr (sizeof(T) == 4) {
         if (waves == 8) return launch_small_nw<T, 8>(a, a_kc, b_kc, batch, stream);
-        if (waves == 16) return launch_small_nw<T, 16>(a, a_kc, b_kc, batch, stream);
     }
     return hipErrorInvalidValue;
 }

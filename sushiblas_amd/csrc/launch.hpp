@@ -16,7 +16,7 @@ template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, i
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream);
 
 // One-launch GEMM for small problems (gemm_small.hip): 32x32 tiles of C,
-// the `waves` (4; 8 or 16 for fp32) waves of a workgroup cutting K that many ways;
+// the `waves` (4, or 8 for fp32) waves of a workgroup cutting K that many ways;
 // a.tiles_m/tiles_n count 32-wide tiles.
 template <typename T>
 hipError_t launch_small(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream,

@@ -75,7 +75,6 @@ enum Cfg {
     F32_SMALL,     // small problems: 32x32 tiles, K cut over the 4 waves (gemm_small.hip)
     F64_SMALL,
     F32_SMALL8,    // the same with K cut over 8 waves
-    F32_SMALL16,   // fp32: the same with K cut over 16 waves (4 per SIMD)
     GENERIC,
 };
 
@@ -97,7 +96,6 @@ const CfgInfo kCfg[] = {
     {"mfma_f64_64x128x16_w2x2", 64, 128, 16, 2},   {"mfma_f64_64x64x16_w2x2", 64, 64, 16, 2},
     {"mfma_f32_32x32_ksplit4", 32, 32, 32, 1},
     {"mfma_f64_32x32_ksplit4", 32, 32, 32, 1},     {"mfma_f32_32x32_ksplit8", 32, 32, 32, 1},
-    {"mfma_f32_32x32_ksplit16", 32, 32, 32, 1},
     {"generic_64x64x16", 64, 64, 16, 4},
 };
 static_assert(sizeof(kCfg) / sizeof(kCfg[0]) == GENERIC + 1, "one kCfg entry per Cfg, in order");
@@ -107,14 +105,14 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // The small-problem kernel's forms (gemm_small.hip).
 inline bool is_small(Cfg c)
 {
-    return c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8 || c == F32_SMALL16;
+    return c == F32_SMALL || c == F64_SMALL || c == F32_SMALL8;
 }
 
 // Tile configurations worth modelling for a problem, the default first; cus
 // is the device's CU count (the round size of one-per-CU tiles).  *large is
 // set for the large-fp32 candidates, whose model adds an epilogue term.  At
-// most kMaxCands are written (the fp32 branch of mid-size shapes has eight).
-constexpr int kMaxCands = 8;
+// most kMaxCands are written (the fp32 branch of mid-size shapes has seven).
+constexpr int kMaxCands = 7;
 int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* out, bool* large)
 {
     *large = false;
@@ -196,16 +194,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         if (f32) out[c++] = F32_64x64;
     }
     out[c++] = f32 ? F32_SMALL : F64_SMALL;
-    // the 8- and 16-wave forms cut K over two and four times the waves: they
-    // shorten each wave's chain of dependent loads where few tiles share a
-    // CU (512^2 x 2048: 15.5 and 13.3 against 17.9 us).  Only one 16-wave
-    // workgroup fits on a CU (its registers), so past one round of tiles the
-    // 8-wave form, up to three per CU, keeps the lead (1024^2 x 512: 14.4
-    // against 19.2 us)
-    if (f32) {
-        out[c++] = F32_SMALL8;
-        out[c++] = F32_SMALL16;
-    }
+    // the 8-wave form cuts K over twice the waves: it shortens each wave's
+    // chain of dependent loads where few tiles share a CU (512^3: 6.45 ->
+    // 6.19 us, 256^2 x 4096: 37.6 -> 29.2 us)
+    if (f32) out[c++] = F32_SMALL8;
     return c;
 }
 
@@ -345,7 +337,7 @@ double cfg_eff(Cfg c)
 constexpr double kEpiSec = 2.2496e-13;
 
 // The small-problem kernel (one launch of 32x32 tiles, w = 2*32*32*K flops
-// each), per form -- fp32 with K cut over 4, 8 or 16 waves, fp64 over 4: a
+// each), per form -- fp32 with K cut over 4 or 8 waves, fp64 over 4: a
 // launch cost `sec`; a workgroup alone on a CU computes at `rs`, up to `occ`
 // of them overlap on one CU, and past that the CU's rate `rc` limits; each
 // workgroup adds `wg`; the operand bytes over kSmallBw (kSmallBwBatch for a
@@ -368,7 +360,6 @@ struct SmallForm {
 };
 constexpr SmallForm kSmallF32W4{2.8336e-06, 4.5870e-07, 2.9187e+11, 3.4076e+11, 2};
 constexpr SmallForm kSmallF32W8{2.7012e-06, 5.0971e-07, 4.8464e+11, 3.5333e+11, 1};
-constexpr SmallForm kSmallF32W16{2.7012e-06, 5.0971e-07, 4.8464e+11, 3.5333e+11, 1};
 constexpr SmallForm kSmallF64W4{3.1395e-06, 1.0982e-06, 4.2042e+11, 1.8879e+11, 2};
 constexpr double kSmallLayF32[2][2] = {{1.0, 1.0856}, {0.9772, 1.0096}};
 constexpr double kSmallLayF64[2][2] = {{1.0, 1.0486}, {1.0604, 0.9434}};
@@ -420,10 +411,7 @@ size_t split_bytes(const Problem& p, Cfg c, const SplitSpace& ss, int64_t split)
 double small_seconds(const Problem& p, Cfg c, int64_t cus, const SplitSpace& ss)
 {
     const bool f64 = c == F64_SMALL;
-    const SmallForm& f = f64                ? kSmallF64W4
-                         : c == F32_SMALL8  ? kSmallF32W8
-                         : c == F32_SMALL16 ? kSmallF32W16
-                                            : kSmallF32W4;
+    const SmallForm& f = f64 ? kSmallF64W4 : c == F32_SMALL8 ? kSmallF32W8 : kSmallF32W4;
     const int akc = !p.ta, bkc = p.tb;
     const double lay = f64 ? kSmallLayF64[akc][bkc] : kSmallLayF32[akc][bkc];
     const int64_t units = tile_count(p, c) * ss.nb;
@@ -630,8 +618,6 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_small(a, akc, bkc, nb, s, 4);
     case F32_SMALL8:
         return launch_small(a, akc, bkc, nb, s, 8);
-    case F32_SMALL16:
-        return launch_small(a, akc, bkc, nb, s, 16);
     default:
         a.tiles_m = (int)cdiv(p.m, 64);
         a.tiles_n = (int)cdiv(p.n, 64);

@@ -414,15 +414,14 @@ def test_three_per_cu_tile_whole_and_split(cuda, layout, ta, tb):
         assert err <= TOL[np.float32], (m, n, k, plan)
 
 
-# -- the small-problem kernel with K cut over 8 or 16 waves ---------------------
+# -- the small-problem kernel with K cut over 8 waves ---------------------------
 
-@pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit8", "mfma_f32_32x32_ksplit16"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_small_kernel_more_waves(cuda, ta, tb, plan):
-    """The small-problem kernel's 8- and 16-wave forms, run by name: 512^3,
-    and a ragged 300 x 200 x 1001 with padded leading dimensions and
-    misaligned bases (K tail, partial tiles); C outside the window
-    untouched."""
+def test_small_kernel_eight_waves(cuda, ta, tb):
+    """The small-problem kernel's 8-wave form, run by name: 512^3, and a
+    ragged 300 x 200 x 1001 with padded leading dimensions and misaligned
+    bases (K tail, partial tiles); C outside the window untouched."""
+    plan = "mfma_f32_32x32_ksplit8"
     for i, (m, n, k, pad, off) in enumerate([(512, 512, 512, (0, 0, 0), (0, 0, 0)),
                                              (300, 200, 1001, (3, 1, 5), (1, 2, 3))]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 90 + i, pad)
@@ -435,8 +434,7 @@ def test_small_kernel_more_waves(cuda, ta, tb, plan):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
-@pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit4", "mfma_f32_32x32_ksplit8",
-                                  "mfma_f32_32x32_ksplit16"])
+@pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit4", "mfma_f32_32x32_ksplit8"])
 def test_small_kernel_tile_order(cuda, plan):
     """Shapes whose tile count is a multiple of 8, where the small-problem
     kernel renumbers its tiles XCD by XCD in columns G tiles tall: 16 x 16
