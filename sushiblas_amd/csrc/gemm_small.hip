@@ -37,6 +37,20 @@ constexpr int stage_groups()
     return NW == 8 ? 2 : 4;
 }
 
+// n / d for n < 2^22, d > 0: the float quotient through the hardware
+// reciprocal (1 ulp) is within 1 of the integer one, and one correction
+// each way makes it exact.  The integer division the compiler would emit
+// takes about 40 scalar instructions, which every wave of a CU issues
+// through the CU's one scalar unit before its first load.
+__device__ inline unsigned udiv22(unsigned n, unsigned d)
+{
+    unsigned q = (unsigned)((float)n * __builtin_amdgcn_rcpf((float)d));
+    const int r = (int)(n - q * d);
+    if (r < 0) --q;
+    else if (r >= (int)d) ++q;
+    return q;
+}
+
 // One element of T from a raw buffer load (4 or 8 bytes).
 __device__ inline float load_elem(float*, __amdgpu_buffer_rsrc_t r, int off)
 {
@@ -136,30 +150,34 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane % MB, q = lane / MB;
     // grid (tiles_m, tiles_n, batch).  The hardware deals workgroups to the
-    // 8 XCDs round-robin by linear index, each XCD with its own L2.  When an
-    // entry's tile count is a multiple of 8 (so that every entry deals
-    // alike), the tiles are renumbered so that XCD j takes the j-th eighth of
-    // them, walked in columns G tiles tall: an XCD then covers about a
-    // sqrt(tiles / 8)-wide square, whose A and B panels its L2 shares,
-    // instead of every column of tiles (512^2 x 2048: 17.9 against 21.2 us
-    // on the 4-wave form, 14.5 against 15.5 on the 8-wave one)
+    // 8 XCDs round-robin by linear index, each XCD with its own L2.  For a
+    // long K, when an entry's tile count is a multiple of 8 (so that every
+    // entry deals alike), the tiles are renumbered so that XCD j takes the
+    // j-th eighth of them, walked in columns G tiles tall: an XCD then covers
+    // about a sqrt(tiles / 8)-wide square, whose A and B panels its L2
+    // shares, instead of every column of tiles (512^2 x 2048: 17.9 against
+    // 21.2 us on the 4-wave form, 14.5 against 15.5 on the 8-wave one).
+    // Below K = 1024 the renumbering's scalar work, done by every wave before
+    // its first load, cost more than the L2 saved (512^3: first loads 0.2 us
+    // later).
     int tm = (int)blockIdx.x, tn = (int)blockIdx.y;
-    {
+    if (K >= 1024) {
         const unsigned gx = (unsigned)(M + kTile - 1) / kTile;  // gridDim.x
         const unsigned gy = (unsigned)(N + kTile - 1) / kTile;  // gridDim.y
         const unsigned tiles = gx * gy;
-        if ((tiles & 7u) == 0 && tiles > 8) {
+        if ((tiles & 7u) == 0 && tiles > 8 && tiles <= (1u << 22)) {
             const unsigned lin = (unsigned)tm + gx * (unsigned)tn;
             const unsigned eighth = tiles >> 3;
             const unsigned id = (lin & 7u) * eighth + (lin >> 3);
             const unsigned G = 1u << ((31 - __builtin_clz(eighth)) >> 1);  // ~sqrt(eighth)
             const unsigned span = G * gy;
-            const unsigned grp = id / span;
+            const unsigned grp = udiv22(id, span);
             const unsigned first = grp * G;
             const unsigned gs = min(gx - first, G);
             const unsigned in = id - grp * span;
-            tm = (int)(first + in % gs);
-            tn = (int)(in / gs);
+            const unsigned col = udiv22(in, gs);
+            tm = (int)(first + in - col * gs);
+            tn = (int)col;
         }
     }
     const int m0 = tm * kTile, n0 = tn * kTile;
