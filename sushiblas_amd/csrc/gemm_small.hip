@@ -37,18 +37,19 @@ constexpr int stage_groups()
     return NW == 8 ? 2 : 4;
 }
 
-// n / d for n < 2^22, d > 0: the float quotient through the hardware
-// reciprocal (1 ulp) is within 1 of the integer one, and one correction
-// each way makes it exact.  The integer division the compiler would emit
-// takes about 40 scalar instructions, which every wave of a CU issues
-// through the CU's one scalar unit before its first load.
+// n / d for wave-uniform n < 2^22, d > 0: the float quotient through the
+// hardware reciprocal (1 ulp) is within 1 of the integer one, and one
+// correction each way makes it exact.  The integer division the compiler
+// would emit takes about 40 scalar instructions, which every wave of a CU
+// issues through the CU's one scalar unit before its first load.  The
+// quotient is read back through readfirstlane so that the compiler keeps
+// what is built from it (the buffer descriptors) in scalar registers.
 __device__ inline unsigned udiv22(unsigned n, unsigned d)
 {
-    unsigned q = (unsigned)((float)n * __builtin_amdgcn_rcpf((float)d));
+    const unsigned q = (unsigned)__builtin_amdgcn_readfirstlane(
+        (int)(unsigned)((float)n * __builtin_amdgcn_rcpf((float)d)));
     const int r = (int)(n - q * d);
-    if (r < 0) --q;
-    else if (r >= (int)d) ++q;
-    return q;
+    return q + (unsigned)(r >= (int)d) - (unsigned)(r < 0);
 }
 
 // One element of T from a raw buffer load (4 or 8 bytes).

@@ -436,18 +436,18 @@ def test_small_kernel_eight_waves(cuda, ta, tb):
 
 @pytest.mark.parametrize("plan", ["mfma_f32_32x32_ksplit4", "mfma_f32_32x32_ksplit8"])
 def test_small_kernel_tile_order(cuda, plan):
-    """Shapes whose tile count is a multiple of 8, where the small-problem
-    kernel renumbers its tiles XCD by XCD in columns G tiles tall: 16 x 16
-    tiles (G = 4), 9 x 8 ragged tiles (G = 2, the last column group one tile
-    tall), 2 x 128 (a group taller than the matrix), each with a transposed
-    operand; then a strided batch of 3 entries of 2 x 8 tiles.  Every tile
-    of C matches the oracle and C's padding is untouched, so no tile is
-    skipped or written twice."""
+    """Shapes with K >= 1024 whose tile count is a multiple of 8, where the
+    small-problem kernel renumbers its tiles XCD by XCD in columns G tiles
+    tall: 16 x 16 tiles (G = 4), 9 x 8 ragged tiles (G = 2, the last column
+    group one tile tall), 2 x 128 (a group taller than the matrix), each
+    with a transposed operand; then a strided batch of 3 entries of 2 x 8
+    tiles.  Every tile of C matches the oracle and C's padding is untouched,
+    so no tile is skipped or written twice."""
     import torch
     import sushiblas_amd as sbx
-    for i, (m, n, k, ta, tb) in enumerate([(512, 512, 701, 0, 0), (283, 253, 300, 0, 1),
-                                           (283, 253, 300, 1, 0), (64, 4096, 256, 0, 0),
-                                           (64, 4096, 256, 1, 1)]):
+    for i, (m, n, k, ta, tb) in enumerate([(512, 512, 1031, 0, 0), (283, 253, 1100, 0, 1),
+                                           (283, 253, 1100, 1, 0), (64, 4096, 1024, 0, 0),
+                                           (64, 4096, 1024, 1, 1)]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 95 + i,
                                              pad=(1, 2, 3))
         print(f"tile-order case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
@@ -457,7 +457,7 @@ def test_small_kernel_tile_order(cuda, plan):
         assert normwise(0, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k, ta, tb)
         outside = (np.arange(C.size) % ldc) >= n
         np.testing.assert_array_equal(got[outside], C[outside])
-    batch, m, n, k = 3, 64, 256, 200
+    batch, m, n, k = 3, 64, 256, 1024
     str_a, str_b, str_c = m * k + 5, k * n + 3, m * n + 7
     A = oracle.fill_uniform(batch * str_a, np.float32, SEED + 99, 0)
     B = oracle.fill_uniform(batch * str_b, np.float32, SEED + 99, 1)
