@@ -130,8 +130,10 @@ struct SmallOperand {
 // is -1 for a strided launch, else the grouped launch's operand swap (0/1),
 // whose device table comes from p.  Everything the epilogue needs -- C, its
 // strides, the scalars -- is read from p after the k loop, so no wait for
-// it stands before the operand loads.
-template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL>
+// it stands before the operand loads.  BETA: beta != 0 (C is read); the
+// beta = 0 form has no trace of the C loads, whose run-time test and index
+// work slowed it by 1-6 % at short K.
+template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL, bool BETA>
 __global__ void __launch_bounds__(NW * 64)
 gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K, int group,
                   int64_t str_a, int64_t str_b, GemmArgs<T> p)
@@ -265,6 +267,22 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     }
     probe_mark(p, 2);  // this wave's MFMAs issued
 
+    // each lane finishes PER = 1024 / (64 NW) elements of the 32x32 tile:
+    // element e = u*64*NW + tid of the partial-tile layout below
+    constexpr int PER = kTile * kTile / (NW * 64);
+    auto c_index = [&](int u, int& m, int& n) {
+        const int e = u * (NW * 64) + tid;
+        const int el = e & 63, r = (e >> 6) % NACC, blk = (e >> 6) / NACC;
+        m = m0 + (blk / NB) * MB + MF::row(r, el / MB);
+        n = n0 + (blk % NB) * MB + el % MB;
+    };
+    typedef __attribute__((address_space(1))) T GlobalT;
+    auto c_base = [&]() {
+        T* C = group >= 0 ? static_cast<T*>(const_cast<void*>(p.table[3 * z + 2]))
+                          : p.C + z * p.str_c;
+        return (GlobalT*)C;
+    };
+
     // partial tiles -> LDS, element (bi, bj, r, lane) at ((bi*NB + bj)*NACC + r)*64 + lane
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi)
@@ -273,28 +291,54 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
 #pragma unroll
             for (int r = 0; r < NACC; ++r)
                 red[wave * PART + ((bi * NB + bj) * NACC + r) * 64 + lane] = acc[bi][bj][r];
+
+    // With beta != 0 this lane's old C values are loaded now, between the
+    // partial tiles' writes and the barrier, so that their latency overlaps
+    // the wait for the slowest wave (loaded after the barrier, each was a
+    // dependent round trip to memory: 37x1000x300, 4 waves, 6.4 -> 5.5 us).
+    // The details matter to the compiler:
+    //  * after the writes, whose accumulators are then dead (a branch while
+    //    they lived made it copy all of them);
+    //  * a lane whose element lies outside C reads the tile's first element
+    //    (in C) and discards it (masked loads merged with a default made it
+    //    wait for the first load before issuing the next);
+    //  * a global-address-space pointer (a flat load would also count in the
+    //    LDS writes' wait before the barrier, which would then wait for C).
+    // Without BETA, C's address is formed after the barrier, as the stores
+    // need it (formed before it, fp64 256^3 ran 3 % slower).
+    GlobalT* Cg = nullptr;
+    [[maybe_unused]] T c_old[PER];  // BETA only
+    if constexpr (BETA) {
+        Cg = c_base();
+        const int64_t ldc = p.ldc;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            int m, n;
+            c_index(u, m, n);
+            const bool in = m < M && n < N;
+            c_old[u] = Cg[in ? (int64_t)m * ldc + n : (int64_t)m0 * ldc + n0];
+        }
+    }
+
     __syncthreads();
 
-    // each lane finishes 1024 / (64 NW) elements of the 32x32 tile, summing
-    // the waves' partials in wave order
-    T* C = group >= 0 ? static_cast<T*>(const_cast<void*>(p.table[3 * z + 2])) : p.C + z * p.str_c;
+    // the waves' partials summed in wave order
+    if constexpr (!BETA) Cg = c_base();
     const int64_t ldc = p.ldc;
-    const T alpha = p.alpha, beta = p.beta;
+    const T alpha = p.alpha;
     const int relu = p.relu;
 #pragma unroll
-    for (int u = 0; u < kTile * kTile / (NW * 64); ++u) {
+    for (int u = 0; u < PER; ++u) {
         const int e = u * (NW * 64) + tid;
-        const int el = e & 63, r = (e >> 6) % NACC, blk = (e >> 6) / NACC;
         T sum = red[e];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sum += red[w * PART + e];
-        const int row = (blk / NB) * MB + MF::row(r, el / MB), col = (blk % NB) * MB + el % MB;
-        const int m = m0 + row, n = n0 + col;
+        int m, n;
+        c_index(u, m, n);
         if (m < M && n < N) {
-            T* cp = C + (int64_t)m * ldc + n;
             T v = alpha * sum;
-            if (beta != (T)0) v += beta * *cp;
-            *cp = relu ? relu_of(v) : v;
+            if constexpr (BETA) v += p.beta * c_old[u];
+            Cg[(int64_t)m * ldc + n] = relu ? relu_of(v) : v;
         }
     }
     probe_mark(p, 3);  // C stores issued
@@ -303,6 +347,14 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
 }  // namespace
 
 namespace {
+template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL, bool BETA>
+void launch_one(dim3 grid, dim3 block, hipStream_t stream, const GemmArgs<T>& a)
+{
+    gemm_small_kernel<T, NW, A_KC, B_KC, KTAIL, BETA><<<grid, block, 0, stream>>>(
+        a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, a.table ? a.table_swap : -1, a.str_a,
+        a.str_b, a);
+}
+
 template <typename T, int NW>
 hipError_t launch_small_nw(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch,
                            hipStream_t stream)
@@ -313,10 +365,10 @@ hipError_t launch_small_nw(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch
     // keeps a 32-row tile's offsets, so ld itself, far below 2^31)
     if (a.lda > INT32_MAX || a.ldb > INT32_MAX) return hipErrorInvalidValue;
     const bool tail = (a_kc || b_kc) && a.K % (16 / (int)sizeof(T)) != 0;
-#define SBX_LAUNCH(AK, BKC, TAIL) \
-    gemm_small_kernel<T, NW, AK, BKC, TAIL><<<grid, block, 0, stream>>>(                  \
-        a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, a.table ? a.table_swap : -1, a.str_a,  \
-        a.str_b, a)
+    const bool beta = a.beta != (T)0;
+#define SBX_LAUNCH(AK, BKC, TAIL)                                                  \
+    (beta ? launch_one<T, NW, AK, BKC, TAIL, true>(grid, block, stream, a)         \
+          : launch_one<T, NW, AK, BKC, TAIL, false>(grid, block, stream, a))
     if (a_kc && b_kc) {
         if (tail) SBX_LAUNCH(true, true, true);
         else SBX_LAUNCH(true, true, false);
