@@ -440,14 +440,17 @@ def test_small_kernel_tile_order(cuda, plan):
     small-problem kernel renumbers its tiles XCD by XCD in columns G tiles
     tall: 16 x 16 tiles (G = 4), 9 x 8 ragged tiles (G = 2, the last column
     group one tile tall), 2 x 128 (a group taller than the matrix), each
-    with a transposed operand; then a strided batch of 3 entries of 2 x 8
-    tiles.  Every tile of C matches the oracle and C's padding is untouched,
+    with a transposed operand; 16 x 1 and 3 x 8 (G = 1), 40 x 8 (G = 4) and
+    13 x 24 (G = 4, the last group one tile tall); then a strided batch of
+    3 entries of 2 x 8 tiles.  Every tile of C matches the oracle and C's padding is untouched,
     so no tile is skipped or written twice."""
     import torch
     import sushiblas_amd as sbx
     for i, (m, n, k, ta, tb) in enumerate([(512, 512, 1031, 0, 0), (283, 253, 1100, 0, 1),
                                            (283, 253, 1100, 1, 0), (64, 4096, 1024, 0, 0),
-                                           (64, 4096, 1024, 1, 1)]):
+                                           (64, 4096, 1024, 1, 1), (512, 32, 1024, 0, 0),
+                                           (96, 256, 1030, 1, 1), (1280, 256, 1024, 0, 1),
+                                           (416, 768, 1024, 1, 0)]):
         A, lda, B, ldb, C, ldc = make_inputs(np.float32, 0, ta, tb, m, n, k, SEED + 95 + i,
                                              pad=(1, 2, 3))
         print(f"tile-order case {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
