@@ -211,6 +211,10 @@ struct GemmArgs {
     // Host side only: which operand the launch loads non-temporally (0
     // none, 1 A, 2 B), picking the kernel's STREAM variant.
     int stream_op;
+    // Host side only, small-problem kernel's 8-wave form: run the variant
+    // whose two waves sharing each SIMD take turns at the higher issue
+    // priority (set for one-round grids with K >= 1024).
+    int alt_prio;
 #ifdef SBX_PROBE
     // Probe build only: per-workgroup timestamps of this dispatch (see
     // ProbeClock), for workgroups [0, stamp_blocks) of batch entry 0.

@@ -132,8 +132,9 @@ struct SmallOperand {
 // strides, the scalars -- is read from p after the k loop, so no wait for
 // it stands before the operand loads.  BETA: beta != 0 (C is read); the
 // beta = 0 form has no trace of the C loads, whose run-time test and index
-// work slowed it by 1-6 % at short K.
-template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL, bool BETA>
+// work slowed it by 1-6 % at short K.  ALT (8 waves only): the two waves
+// sharing each SIMD take turns at the higher issue priority, stage by stage.
+template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL, bool BETA, bool ALT>
 __global__ void __launch_bounds__(NW * 64)
 gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K, int group,
                   int64_t str_a, int64_t str_b, GemmArgs<T> p)
@@ -250,20 +251,52 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     const int n = (ke - k0 + kStageK - 1) / kStageK;
     if (n > 0) issue(0, k0);
     probe_mark(p, 1);  // first stage's loads issued
-    int done = 0;  // stages consumed
-    for (; done + 2 < n; done += 2) {
-        issue(1, k0 + kStageK);
-        mma(0);
-        issue(0, k0 + 2 * kStageK);
-        mma(1);
-        k0 += 2 * kStageK;
-    }
-    if (n - done == 2) {
-        issue(1, k0 + kStageK);
-        mma(0);
-        mma(1);
-    } else if (n - done == 1) {
-        mma(0);
+    // With ALT the two waves sharing each SIMD (w and w + 4) take turns at
+    // the higher issue priority, one stage each: under the default
+    // oldest-first issue one runs ahead and the other finishes alone, its
+    // loads no longer hidden behind its partner's MFMAs.  Each half of the
+    // workgroup runs its own copy of the loop, so that no branch splits a
+    // stage's loads from the MFMAs the compiler interleaves them with (a
+    // run-time test there slowed the loop even with the turns off).
+    auto run = [&](auto first) {
+        constexpr bool F = decltype(first)::value;
+        auto favour = [&](int stage) {
+            if constexpr (ALT) {
+                if constexpr (F) {
+                    if (stage == 0) __builtin_amdgcn_s_setprio(1);
+                    else __builtin_amdgcn_s_setprio(0);
+                } else {
+                    if (stage == 0) __builtin_amdgcn_s_setprio(0);
+                    else __builtin_amdgcn_s_setprio(1);
+                }
+            }
+        };
+        int done = 0;  // stages consumed
+        for (; done + 2 < n; done += 2) {
+            issue(1, k0 + kStageK);
+            favour(0);
+            mma(0);
+            issue(0, k0 + 2 * kStageK);
+            favour(1);
+            mma(1);
+            k0 += 2 * kStageK;
+        }
+        if (n - done == 2) {
+            issue(1, k0 + kStageK);
+            favour(0);
+            mma(0);
+            favour(1);
+            mma(1);
+        } else if (n - done == 1) {
+            mma(0);
+        }
+        if constexpr (ALT) __builtin_amdgcn_s_setprio(0);
+    };
+    if constexpr (ALT) {
+        if ((wave >> 2) == 0) run(std::true_type{});
+        else run(std::false_type{});
+    } else {
+        run(std::true_type{});
     }
     probe_mark(p, 2);  // this wave's MFMAs issued
 
@@ -350,9 +383,16 @@ namespace {
 template <typename T, int NW, bool A_KC, bool B_KC, bool KTAIL, bool BETA>
 void launch_one(dim3 grid, dim3 block, hipStream_t stream, const GemmArgs<T>& a)
 {
-    gemm_small_kernel<T, NW, A_KC, B_KC, KTAIL, BETA><<<grid, block, 0, stream>>>(
-        a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, a.table ? a.table_swap : -1, a.str_a,
-        a.str_b, a);
+    const int group = a.table ? a.table_swap : -1;
+    if constexpr (NW == 8) {
+        if (a.alt_prio) {
+            gemm_small_kernel<T, NW, A_KC, B_KC, KTAIL, BETA, true><<<grid, block, 0, stream>>>(
+                a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, group, a.str_a, a.str_b, a);
+            return;
+        }
+    }
+    gemm_small_kernel<T, NW, A_KC, B_KC, KTAIL, BETA, false><<<grid, block, 0, stream>>>(
+        a.A, a.B, (int)a.lda, (int)a.ldb, a.M, a.N, a.K, group, a.str_a, a.str_b, a);
 }
 
 template <typename T, int NW>

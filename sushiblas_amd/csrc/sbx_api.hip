@@ -921,6 +921,12 @@ int run(const Problem& p, T alpha, T beta, int algo, hipStream_t stream, Cfg* ch
             a.table = p.table ? p.table + 3 * b0 : nullptr;
             a.table_swap = p.table_swap;
             a.stream_op = stream_operand(p, a.tiles_m, a.tiles_n);
+            // the 8-wave small-problem kernel's pairs of waves take turns at
+            // the higher issue priority where each CU holds one workgroup
+            // and K is long (512^2 x 2048: 13.7 against 14.6 us; on grids of
+            // several rounds it lost, 1024^2 x 512: 16.9 against 14.1 us)
+            a.alt_prio = cfg == F32_SMALL8 && p.k >= 1024 &&
+                         (int64_t)a.tiles_m * a.tiles_n * nb <= cu_count();
 #ifdef SBX_PROBE
             probe_assign(a);
 #endif
