@@ -153,6 +153,13 @@ struct LdsVec<float, 4> {
     }
 };
 template <>
+struct LdsVec<float, 3> {  // 12-byte aligned at best: element reads
+    __device__ static inline void read(const float* p, float* o)
+    {
+        o[0] = p[0]; o[1] = p[1]; o[2] = p[2];
+    }
+};
+template <>
 struct LdsVec<double, 1> {
     __device__ static inline void read(const double* p, double* o) { o[0] = *p; }
 };
@@ -441,9 +448,13 @@ struct Frag {
     // LDS read instructions per k group: a k-contiguous tile takes one
     // 16-byte read per block; an x-contiguous one NB/U*V reads of U elements,
     // which the compiler pairs into ds_read2 instructions when they are
-    // narrower than 16 bytes (rows kk and kk+1 lie LD elements apart)
-    static constexpr int INSTR =
-        KC ? NB : (NB / U * V) / (U * (int)sizeof(T) < 16 ? 2 : 1);
+    // narrower than 16 bytes (rows kk and kk+1 lie LD elements apart), and
+    // U = 3 (12 bytes at 4-byte alignment) takes two instructions each
+    // (counted as one, the hint pattern missed most of them and the 48-column
+    // tile ran 343 against 221 us at 65536 x 48 x 4096)
+    static constexpr int INSTR = KC       ? NB
+                                 : U == 3 ? (NB / U * V) * 2
+                                          : (NB / U * V) / (U * (int)sizeof(T) < 16 ? 2 : 1);
 
     // Read the fragments of k-group g (KG k values) for wave offset w0.
     // f[b][kk] is block b's operand for MFMA step kk.
@@ -615,8 +626,12 @@ __device__ inline void hints_b()
 // WPE: waves per SIMD the register budget is sized for (1 or 2).
 // MI: MFMA shape (see Mfma; fp32 only has a choice).
 // STREAM: the operand whose loads are non-temporal (0 none, 1 A, 2 B).
+// BNC: columns of the tile that are computed (default BN).  BNC < BN loads a
+// BN-wide B tile but runs MFMAs and keeps accumulators for its first BNC
+// columns only: the host uses it where N <= BNC (one tile column), so a
+// 48-wide C does not pay for 64 columns of MFMAs.
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          bool KTAIL, int PF, int WPE, int MI = 0, int STREAM = 0>
+          bool KTAIL, int PF, int WPE, int MI = 0, int STREAM = 0, int BNC = BN>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
@@ -624,8 +639,9 @@ gemm_mfma_kernel(GemmArgs<T> p)
     constexpr int MB = MF::MB;
     constexpr int V = MF::V;
     constexpr int KG = MF::Q * V;  // k values per group
-    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int WTM = BM / WAVES_M, WTN = BNC / WAVES_N;
     constexpr int NBM = WTM / MB, NBN = WTN / MB;
+    static_assert(BNC <= BN && BNC % (WAVES_N * MB) == 0, "computed columns: whole blocks of BN");
     constexpr int G = BK / KG;  // k groups per tile
     constexpr int NTHR = WAVES_M * WAVES_N * 64;
     static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");

@@ -63,6 +63,7 @@ enum Cfg {
     F32_128x128_O3,  // the same tile at 3 waves/SIMD (three workgroups per CU)
     F32_128x64,    // n <= 64 (tall-skinny): 4 waves of 64x32, 2 tiles in flight
     F32_256x64,    // n <= 64 with a full round of 256-row tiles: 8 waves of 32x64 (16x16x4 MFMAs)
+    F32_256x48,    // 32 < n <= 48: the 256x64 tile computing 48 columns (waves of 32x48)
     F32_64x128,    // m <= 64
     F32_64x256,    // m <= 64 with a full round of 256-column tiles: 8 waves of 64x32 (16x16x4 MFMAs)
     F32_128x32,    // n <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
@@ -89,6 +90,7 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x128x16_w2x2", 128, 128, 16, 2},
     {"mfma_f32_128x128x16_w2x2_o3", 128, 128, 16, 3},
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
+    {"mfma_f32_256x48x32_w8x1", 256, 64, 32, 1},  // bn: the loaded (and workspace) width
     {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},   {"mfma_f32_64x256x32_w1x8", 64, 256, 32, 1},
     {"mfma_f32_128x32x32_w4x1", 128, 32, 32, 2},   {"mfma_f32_32x128x32_w1x4", 32, 128, 32, 2},
     {"mfma_f32_64x64x32_w2x2", 64, 64, 32, 2},
@@ -140,6 +142,10 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         // where a 32-wide one streams A at up to 5.9 TB/s (65536 x 32 x
         // 4096: 183 against 272 us; 40000 x 32 x 2048: 76 against 85 us)
         if (f32 && n <= 32) out[c++] = F32_128x32;
+        // 32 < n <= 48: the 256-row tile computing 48 of its 64 columns, 3/4
+        // of the MFMAs of the 64-wide tiles (65536 x 48 x 4096: 263 us on
+        // 256x64 against 218 for the vendor)
+        if (f32 && n > 32 && n <= 48) out[c++] = F32_256x48;
         // one 8-wave 256-row workgroup per CU: B is read by half as many
         // workgroups (65536 x 64 x 4096: 291-294 us against 296-300)
         if (f32 && cdiv(m, 256) >= cus) out[c++] = F32_256x64;
@@ -215,6 +221,8 @@ bool mfma_feasible(const Problem& p, Cfg c)
     // the small-problem kernel's grid is (tiles along m, tiles along n, batch)
     if (is_small(c) && cdiv(p.n, ci.bn) > 65535)
         return false;
+    // computes 48 columns of its single tile column
+    if (c == F32_256x48 && p.n > 48) return false;
     const size_t elem = p.dtype == SBX_F32 ? 4 : 8;
     return offsets_fit(!p.ta, ci.bm, ci.bk, p.lda, elem) &&
            offsets_fit(p.tb, ci.bn, ci.bk, p.ldb, elem) &&
@@ -321,6 +329,8 @@ double cfg_eff(Cfg c)
     switch (c) {
     case F32_128x128_O3: return 1.0091;
     case F32_128x64: return 0.9656;
+    // the model counts the loaded 64 columns; 48 are computed
+    case F32_256x48: return 64.0 / 48.0;
     case F32_64x128: return 0.9732;
     case F32_64x64: return 0.9478;
     case F32_256x128: return 1.0157;
@@ -604,6 +614,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 128, 64, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_256x64:
         return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2, 1>(a, akc, bkc, nb, s);
+    case F32_256x48:
+        return launch_mfma<float, 256, 64, 32, 8, 1, 2, 2, 1, 48>(a, akc, bkc, nb, s);
     case F32_64x128:
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_64x256:

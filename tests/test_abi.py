@@ -305,3 +305,15 @@ def test_grouped_gemm_validation():
     assert grouped(dtype=5) == 2
     assert grouped(count=0, table=0) == 0  # nothing to do
     assert grouped(m=0) == 0
+
+
+def test_tile_256x48_refused_past_48():
+    """Past 48 columns the 48-column tile is not a plan, and naming it is
+    refused on the host."""
+    plans = [p for p, _ in sbx.gemm_plans(sbx.F32, 0, 0, 0, 4096, 49, 512, 512, 49, 49, 1)]
+    assert not any(p.startswith("mfma_f32_256x48") for p in plans)
+    a = ctypes.c_float(1.0)
+    st = sbx.lib().sbx_gemm_ex_plan(0, 0, 0, 0, 0, 4096, 49, 512, ctypes.byref(a), 16, 512, 0,
+                                    16, 49, 0, ctypes.byref(a), 16, 49, 0, 1,
+                                    b"mfma_f32_256x48x32_w8x1")
+    assert st == 2, st

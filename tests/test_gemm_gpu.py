@@ -482,6 +482,32 @@ def test_small_kernel_tile_order(cuda, plan):
                                       C[b * str_c + m * n:(b + 1) * str_c])
 
 
+# -- the 256x64 tile computing 48 columns (32 < n <= 48) -----------------------
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_tile_256x48(cuda, layout, ta, tb):
+    """The 256x64 tile that computes only its first 48 columns, run by name
+    where C is 33-48 wide (column-major: 33-48 rows): ragged rows, a K tail,
+    padded leading dimensions, beta != 0, unsplit and split in four; C's
+    padding untouched."""
+    for i, (m, n, k, plan) in enumerate([(4097, 48, 515, "mfma_f32_256x48x32_w8x1"),
+                                         (1000, 33, 2049, "mfma_f32_256x48x32_w8x1+splitk4"),
+                                         (300, 45, 64, "mfma_f32_256x48x32_w8x1")]):
+        if layout == 1:
+            m, n = n, m  # the narrow side is m of a column-major C
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, layout, ta, tb, m, n, k, SEED + 110 + i,
+                                             pad=(2, 3, 5))
+        print(f"256x48 case layout={layout} {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        got = run_sbx(cuda, np.float32, layout, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C,
+                      ldc, plan=plan)
+        want = run_oracle(layout, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(layout, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k, plan)
+        inner = n if layout == 0 else m
+        outside = (np.arange(C.size) % ldc) >= inner
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 # -- the large fp32 tiles on ragged edges --------------------------------------
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
