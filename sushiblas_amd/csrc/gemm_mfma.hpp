@@ -629,9 +629,9 @@ __device__ inline void hints_b()
 // BNC: columns of the tile that are computed (default BN).  BNC < BN loads a
 // BN-wide B tile but runs MFMAs and keeps accumulators for its first BNC
 // columns only: the host uses it where N <= BNC (one tile column), so a
-// 48-wide C does not pay for 64 columns of MFMAs.
+// 48-wide C does not pay for 64 columns of MFMAs.  BMC: the same for rows.
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC,
-          bool KTAIL, int PF, int WPE, int MI = 0, int STREAM = 0, int BNC = BN>
+          bool KTAIL, int PF, int WPE, int MI = 0, int STREAM = 0, int BNC = BN, int BMC = BM>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_mfma_kernel(GemmArgs<T> p)
 {
@@ -639,9 +639,10 @@ gemm_mfma_kernel(GemmArgs<T> p)
     constexpr int MB = MF::MB;
     constexpr int V = MF::V;
     constexpr int KG = MF::Q * V;  // k values per group
-    constexpr int WTM = BM / WAVES_M, WTN = BNC / WAVES_N;
+    constexpr int WTM = BMC / WAVES_M, WTN = BNC / WAVES_N;
     constexpr int NBM = WTM / MB, NBN = WTN / MB;
     static_assert(BNC <= BN && BNC % (WAVES_N * MB) == 0, "computed columns: whole blocks of BN");
+    static_assert(BMC <= BM && BMC % (WAVES_M * MB) == 0, "computed rows: whole blocks of BM");
     constexpr int G = BK / KG;  // k groups per tile
     constexpr int NTHR = WAVES_M * WAVES_N * 64;
     static_assert(NTHR == 256 || NTHR == 512, "4 or 8 waves per workgroup");

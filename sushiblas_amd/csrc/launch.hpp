@@ -13,7 +13,7 @@
 namespace sbx {
 
 template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, int MI = 0,
-          int BNC = BN>
+          int BNC = BN, int BMC = BM>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream);
 
 // One-launch GEMM for small problems (gemm_small.hip): 32x32 tiles of C,

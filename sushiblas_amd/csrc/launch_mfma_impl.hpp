@@ -7,7 +7,8 @@
 
 namespace sbx {
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, int MI, int BNC>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int PF, int WPE, int MI, int BNC,
+          int BMC>
 hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hipStream_t stream)
 {
     const int tiles = a.tiles;
@@ -24,10 +25,10 @@ hipError_t launch_mfma(const GemmArgs<T>& a, bool a_kc, bool b_kc, int batch, hi
 #define SBX_LAUNCH(AK, BKC, TAIL)                                                                 \
     do {                                                                                          \
         if (streamed)                                                                             \
-            gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE, MI, kStream, BNC>     \
+            gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE, MI, kStream, BNC, BMC>\
                 <<<grid, block, 0, stream>>>(a);                                                  \
         else                                                                                      \
-            gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE, MI, 0, BNC>           \
+            gemm_mfma_kernel<T, BM, BN, BK, WM, WN, AK, BKC, TAIL, PF, WPE, MI, 0, BNC, BMC>      \
                 <<<grid, block, 0, stream>>>(a);                                                  \
     } while (0)
     if (a_kc && b_kc) {

@@ -66,6 +66,7 @@ enum Cfg {
     F32_256x48,    // 32 < n <= 48: the 256x64 tile computing 48 columns (waves of 32x48)
     F32_64x128,    // m <= 64
     F32_64x256,    // m <= 64 with a full round of 256-column tiles: 8 waves of 64x32 (16x16x4 MFMAs)
+    F32_48x256,    // 32 < m <= 48: the 64x256 tile computing 48 rows (waves of 48x32)
     F32_128x32,    // n <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
     F32_32x128,    // m <= 32: 4 waves of 32x32 (16x16x4 MFMAs)
     F32_64x64,     // fp32 mid-size: 4 waves of 32x32
@@ -92,6 +93,7 @@ const CfgInfo kCfg[] = {
     {"mfma_f32_128x64x32_w2x2", 128, 64, 32, 2},   {"mfma_f32_256x64x32_w8x1", 256, 64, 32, 1},
     {"mfma_f32_256x48x32_w8x1", 256, 64, 32, 1},  // bn: the loaded (and workspace) width
     {"mfma_f32_64x128x32_w2x2", 64, 128, 32, 2},   {"mfma_f32_64x256x32_w1x8", 64, 256, 32, 1},
+    {"mfma_f32_48x256x32_w1x8", 64, 256, 32, 1},  // bm: the loaded (and workspace) height
     {"mfma_f32_128x32x32_w4x1", 128, 32, 32, 2},   {"mfma_f32_32x128x32_w1x4", 32, 128, 32, 2},
     {"mfma_f32_64x64x32_w2x2", 64, 64, 32, 2},
     {"mfma_f64_128x128x16_w2x2", 128, 128, 16, 2}, {"mfma_f64_128x64x16_w2x2", 128, 64, 16, 2},
@@ -161,6 +163,8 @@ int candidate_cfgs(int dtype, int64_t m, int64_t n, int uplo, int64_t cus, Cfg* 
         // the mirror of the tall case (column-major tall-skinny calls land
         // here): 64 x 65536 x 4096 270-272 against 280-284 us for 64x128
         if (f32 && m <= 32) out[c++] = F32_32x128;  // (32 x 65536 x 4096: 166 against 245 us)
+        // the mirror of the 48-column tile
+        if (f32 && m > 32 && m <= 48) out[c++] = F32_48x256;
         if (f32 && cdiv(n, 256) >= cus) out[c++] = F32_64x256;
         out[c++] = wide;
         if (f32) out[c++] = F32_64x64;
@@ -223,6 +227,7 @@ bool mfma_feasible(const Problem& p, Cfg c)
         return false;
     // computes 48 columns of its single tile column
     if (c == F32_256x48 && p.n > 48) return false;
+    if (c == F32_48x256 && p.m > 48) return false;  // and of rows
     const size_t elem = p.dtype == SBX_F32 ? 4 : 8;
     return offsets_fit(!p.ta, ci.bm, ci.bk, p.lda, elem) &&
            offsets_fit(p.tb, ci.bn, ci.bk, p.ldb, elem) &&
@@ -332,6 +337,7 @@ double cfg_eff(Cfg c)
     // the model counts the loaded 64 columns, of which 48 are computed: at
     // 65536 x {33, 40, 48} x 4096 it ran 0.85-0.86 of the 256x64 tile's time
     case F32_256x48: return 1.17;
+    case F32_48x256: return 1.17;  // its mirror, the same counting
     case F32_64x128: return 0.9732;
     case F32_64x64: return 0.9478;
     case F32_256x128: return 1.0157;
@@ -621,6 +627,8 @@ hipError_t launch_cfg(Cfg cfg, GemmArgs<float>& a, bool akc, bool bkc, const Pro
         return launch_mfma<float, 64, 128, 32, 2, 2, 2, 2>(a, akc, bkc, nb, s);
     case F32_64x256:
         return launch_mfma<float, 64, 256, 32, 1, 8, 2, 2, 1>(a, akc, bkc, nb, s);
+    case F32_48x256:
+        return launch_mfma<float, 64, 256, 32, 1, 8, 2, 2, 1, 256, 48>(a, akc, bkc, nb, s);
     case F32_128x32:
         return launch_mfma<float, 128, 32, 32, 4, 1, 2, 2, 1>(a, akc, bkc, nb, s);
     case F32_32x128:

@@ -93,7 +93,7 @@ def test_noop_cases_need_no_device():
     (0, 1, 0, 0, 65536, 64, 4096, "mfma_f32_64x256x32_w1x8"),  # column-major tall-skinny
     (0, 0, 0, 0, 32, 65536, 4096, "mfma_f32_32x128x32_w1x4"),  # m <= 32: 32-row tiles
     (0, 0, 0, 0, 65536, 32, 4096, "mfma_f32_128x32x32_w4x1"),  # n <= 32: 32-column tiles
-    (0, 0, 0, 0, 48, 65536, 4096, "mfma_f32_64x256x32_w1x8"),  # the small kernel would stream B
+    (0, 0, 0, 0, 48, 65536, 4096, "mfma_f32_48x256x32_w1x8"),  # 222 against 252 us (64x256)
     (0, 0, 0, 0, 64, 80000, 2048, "mfma_f32_64x256x32_w1x8+splitk4"),  # 173 us, the fastest
     (1, 0, 0, 0, 8192, 8192, 8192, "mfma_f64_128x128x16_w2x2"),
     (1, 0, 0, 0, 65536, 64, 4096, "mfma_f64_128x64x16_w2x2"),
@@ -316,4 +316,18 @@ def test_tile_256x48_refused_past_48():
     st = sbx.lib().sbx_gemm_ex_plan(0, 0, 0, 0, 0, 4096, 49, 512, ctypes.byref(a), 16, 512, 0,
                                     16, 49, 0, ctypes.byref(a), 16, 49, 0, 1,
                                     b"mfma_f32_256x48x32_w8x1")
+    assert st == 2, st
+
+
+def test_tile_48x256_refused_past_48():
+    """The mirror: past 48 rows the 48-row tile is not a plan, and naming it
+    is refused on the host."""
+    plans = [p for p, _ in sbx.gemm_plans(sbx.F32, 0, 0, 0, 49, 4096, 512, 512, 4096, 4096, 1)]
+    assert not any(p.startswith("mfma_f32_48x256") for p in plans)
+    assert any(p.startswith("mfma_f32_48x256")
+               for p, _ in sbx.gemm_plans(sbx.F32, 0, 0, 0, 48, 4096, 512, 512, 4096, 4096, 1))
+    a = ctypes.c_float(1.0)
+    st = sbx.lib().sbx_gemm_ex_plan(0, 0, 0, 0, 0, 49, 4096, 512, ctypes.byref(a), 16, 512, 0,
+                                    16, 4096, 0, ctypes.byref(a), 16, 4096, 0, 1,
+                                    b"mfma_f32_48x256x32_w1x8")
     assert st == 2, st

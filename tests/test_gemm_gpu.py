@@ -508,6 +508,29 @@ def test_tile_256x48(cuda, layout, ta, tb):
         np.testing.assert_array_equal(got[outside], C[outside])
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_tile_48x256(cuda, layout, ta, tb):
+    """The mirror: the 64x256 tile computing only its first 48 rows, run by
+    name where C has 33-48 rows (column-major: 33-48 columns), with the
+    same ragged edges, K tail, padding, beta != 0 and split."""
+    for i, (m, n, k, plan) in enumerate([(48, 4097, 515, "mfma_f32_48x256x32_w1x8"),
+                                         (33, 1000, 2049, "mfma_f32_48x256x32_w1x8+splitk4"),
+                                         (45, 300, 64, "mfma_f32_48x256x32_w1x8")]):
+        if layout == 1:
+            m, n = n, m
+        A, lda, B, ldb, C, ldc = make_inputs(np.float32, layout, ta, tb, m, n, k, SEED + 120 + i,
+                                             pad=(2, 3, 5))
+        print(f"48x256 case layout={layout} {m}x{n}x{k} t{ta}{tb} -> {plan}", flush=True)
+        got = run_sbx(cuda, np.float32, layout, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C,
+                      ldc, plan=plan)
+        want = run_oracle(layout, ta, tb, m, n, k, 1.25, A, lda, B, ldb, 0.5, C, ldc)
+        assert normwise(layout, got, want, m, n, ldc) <= TOL[np.float32], (m, n, k, plan)
+        inner = n if layout == 0 else m
+        outside = (np.arange(C.size) % ldc) >= inner
+        np.testing.assert_array_equal(got[outside], C[outside])
+
+
 # -- the large fp32 tiles on ragged edges --------------------------------------
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
