@@ -323,6 +323,11 @@ constexpr double kPartSec = 8.200e-7;
 constexpr double kTileSec = 7.824e-7;
 constexpr double kTileStoreBw = 2.2870e10;
 constexpr double kE1 = 0.9944;
+// The same for the 32-wide tiles, which stream their long operand from HBM:
+// alone on a CU a workgroup cannot pull the CU's share of the bandwidth
+// (8192 x 16 x 8192: split in four, one workgroup per CU, 57 us; in eight,
+// two per CU, 51 us, though the split costs more to reduce).
+constexpr double kE1Stream = 0.8;
 
 // Relative MFMA rate of a tile config.  1 for the 128^2 tiles, which the
 // rates are quoted on, for the configs only tall, wide or large shapes reach,
@@ -464,10 +469,11 @@ double plan_seconds(const Problem& p, Cfg c, int64_t cus, const SplitSpace& ss, 
     }
     const double wk = 2.0 * ci.bm * ci.bn * (double)p.k / rate;  // a whole tile's MFMA work
     const double w = wk + o_tile + kTileSec + c_bytes / kTileStoreBw;
-    if (split <= 1 || ss.smax == 0) return rounds_time(ss.tiles * ss.nb, w, P, cus, kE1) + kGridSec;
+    const double e1 = c == F32_128x32 || c == F32_32x128 ? kE1Stream : kE1;
+    if (split <= 1 || ss.smax == 0) return rounds_time(ss.tiles * ss.nb, w, P, cus, e1) + kGridSec;
     const int64_t sp = split;
-    return rounds_time(ss.full * ss.nb, w, P, cus, kE1) +
-           rounds_time(ss.rem * sp * ss.nb, wk / (double)sp + o_part + kPartSec, P, cus, kE1) +
+    return rounds_time(ss.full * ss.nb, w, P, cus, e1) +
+           rounds_time(ss.rem * sp * ss.nb, wk / (double)sp + o_part + kPartSec, P, cus, e1) +
            kGridSec + kReduceSec + (double)(ss.rem * sp * ss.nb) * c_bytes / kReduceBw;
 }
 
