@@ -214,15 +214,16 @@ gemm_small_kernel(const T* A, const T* B, int lda, int ldb, int M, int N, int K,
     constexpr int kStageK = 8 * SG;  // k values per stage
     SmallOperand<T, A_KC, KTAIL, SG> a[2];
     SmallOperand<T, B_KC, KTAIL, SG> b[2];
-    // The 4-wave form's stages (4 groups) issue A's and B's loads group by
-    // group, so that the first MFMAs wait only for their own group's data
-    // (in-order load counters: 512^2 x 2048 17.7 -> 16.2 us, 512^3 6.1 ->
-    // 6.0, bit-identical); the 8-wave form's (2 groups) all of A then all of
-    // B, which measured faster there (512^3 5.5 against 5.9 us interleaved).
+    // The fp32 4-wave form's stages (4 groups) issue A's and B's loads group
+    // by group, so that the first MFMAs wait only for their own group's data
+    // (in-order load counters: 512^2 x 2048 17.7 -> 15.8 us, 512^3 6.2 ->
+    // 6.15, bit-identical); the 8-wave form (2 groups) and fp64 issue all of
+    // A then all of B, which measured faster there (512^3 5.5 against 5.9 us
+    // on 8 waves; fp64 1024^2 x 512 27.4 against 29.1 us).
     auto issue = [&](int st, int k0) {
         const int64_t pa = a_at(k0), pb = b_at(k0);
         const int64_t sa = (a_end - pa) * (int64_t)sizeof(T), sb = (b_end - pb) * (int64_t)sizeof(T);
-        if constexpr (NW == 4) {
+        if constexpr (NW == 4 && sizeof(T) == 4) {
 #pragma unroll
             for (int s = 0; s < SG; ++s) {
                 a[st].load(A + pa, sa, lda, i, q, M - m0, k0, k_lim, K, s);
